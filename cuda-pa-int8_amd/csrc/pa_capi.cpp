@@ -1,0 +1,332 @@
+// extern "C" entry points of libpa_mi355x.so (declared in include/pa_mi355x.h).
+//
+// Host side only: argument validation (the reference's TORCH_CHECKs made
+// device-free), split planning, workspace carving and kernel dispatch.
+#include "pa_mi355x.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "pa_internal.hpp"
+
+namespace {
+
+constexpr int kRefTile = 128;        // reference TILE (paged_attention_v3_warp.cu:20)
+constexpr int kTargetGroups = 1024;  // work-groups one decode launch aims for (256 CUs x 4)
+constexpr int kMinPartition = 256;   // 4 waves x one 64-token iteration
+constexpr int kMaxPartition = 4096;  // caps the serial work of one work-group
+constexpr size_t kAlign = 256;
+
+bool is_f16(pa_decode_kind_t k) { return k == PA_DECODE_WARP_F16 || k == PA_DECODE_SPLITK_F16; }
+bool is_fused(pa_decode_kind_t k) { return k == PA_DECODE_WARP_F16 || k == PA_DECODE_WARP_I8; }
+bool supported_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+int ilog2(int v) {
+  int r = 0;
+  while ((1 << r) < v) ++r;
+  return r;
+}
+
+// Largest divisor of the GQA group size that fits one work-group's head tile.
+int head_tile_for(int group) {
+  for (int t = std::min(group, pa::kMaxGroupTile); t >= 1; --t)
+    if (group % t == 0) return t;
+  return 1;
+}
+
+struct Plan {
+  int head_tile = 1;
+  int nchunk = 1;
+  int units = 0;
+  int partition = 0;
+  int nsplit = 1;
+};
+
+Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_heads,
+               int block_size, int max_blocks, int max_context_len, int partition_tokens) {
+  (void)kind;
+  Plan p;
+  const int group = num_heads / num_kv_heads;
+  p.head_tile = head_tile_for(group);
+  p.nchunk = group / p.head_tile;
+  p.units = num_seqs * num_kv_heads * p.nchunk;
+  const long long cap = (long long)max_blocks * block_size;
+  long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
+  if (ctx < 1) ctx = 1;
+  long long part;
+  if (partition_tokens > 0) {
+    part = partition_tokens;
+  } else {
+    const long long units = std::max(1, p.units);
+    part = (ctx * units + kTargetGroups - 1) / kTargetGroups;
+    part = std::max<long long>(part, kMinPartition);
+    part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
+    part = std::min<long long>(part, kMaxPartition);
+  }
+  part = (part + pa::kIterTokens - 1) / pa::kIterTokens * pa::kIterTokens;
+  part = std::min<long long>(part, (ctx + pa::kIterTokens - 1) / pa::kIterTokens * pa::kIterTokens);
+  p.partition = (int)part;
+  p.nsplit = (int)((ctx + part - 1) / part);
+  return p;
+}
+
+struct WsLayout {
+  size_t counters = 0, ml = 0, acc = 0, total = 0;
+};
+
+WsLayout ws_layout(const Plan& p, int head_dim) {
+  WsLayout w;
+  w.counters = align_up((size_t)p.units * sizeof(uint32_t));
+  w.ml = align_up((size_t)p.units * p.nsplit * p.head_tile * 2 * sizeof(float));
+  w.acc = align_up((size_t)p.units * p.nsplit * p.head_tile * head_dim * sizeof(float));
+  w.total = w.counters + w.ml + w.acc;
+  return w;
+}
+
+pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const void* k_cache,
+                          const void* v_cache, const float* k_scales, const float* v_scales,
+                          const int32_t* block_table, const int32_t* context_lens, float scale,
+                          int32_t block_size, int32_t num_seqs, int32_t num_heads,
+                          int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks, int32_t x,
+                          int32_t max_blocks, int32_t max_context_len, int32_t partition_tokens,
+                          void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+  pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads,
+                                      num_blocks, block_size, x, max_blocks);
+  if (st != PA_OK) return st;
+  if (num_seqs == 0) return PA_OK;
+  if (!out || !q || !k_cache || !v_cache || !block_table || !context_lens) return PA_ERR_NULL_POINTER;
+  if (!is_f16(kind) && (!k_scales || !v_scales)) return PA_ERR_NULL_POINTER;
+
+  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, block_size, max_blocks,
+                           max_context_len, partition_tokens);
+  const WsLayout wl = ws_layout(p, head_dim);
+  if (!workspace || workspace_bytes < wl.total) return PA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0) return PA_ERR_WORKSPACE;
+
+  pa::DecodeLaunch l{};
+  l.out = out;
+  l.q = q;
+  l.k_cache = k_cache;
+  l.v_cache = v_cache;
+  l.k_scales = k_scales;
+  l.v_scales = v_scales;
+  l.block_table = block_table;
+  l.context_lens = context_lens;
+  char* ws = static_cast<char*>(workspace);
+  l.counters = reinterpret_cast<uint32_t*>(ws);
+  l.part_ml = reinterpret_cast<float*>(ws + wl.counters);
+  l.part_acc = reinterpret_cast<float*>(ws + wl.counters + wl.ml);
+  l.head_dim = head_dim;
+  l.head_tile = p.head_tile;
+  l.int8_kv = !is_f16(kind);
+  l.fused = is_fused(kind);
+  l.stream = reinterpret_cast<hipStream_t>(stream);
+  pa::DecodeShape& sh = l.shape;
+  sh.num_seqs = num_seqs;
+  sh.num_heads = num_heads;
+  sh.num_kv_heads = num_kv_heads;
+  sh.group = num_heads / num_kv_heads;
+  sh.nchunk = p.nchunk;
+  sh.block_size = block_size;
+  sh.bs_log2 = ilog2(block_size);
+  sh.num_blocks = num_blocks;
+  sh.max_blocks = max_blocks;
+  sh.partition = p.partition;
+  sh.nsplit = p.nsplit;
+  sh.num_items = num_seqs * num_kv_heads * p.nsplit;
+  sh.scale_log2 = scale * 1.4426950408889634f;
+
+  hipError_t e;
+  switch (head_dim) {
+    case 64: e = pa::launch_decode_d64(l); break;
+    case 128: e = pa::launch_decode_d128(l); break;
+    default: e = pa::launch_decode_d256(l); break;
+  }
+  return e == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pa_status_string(pa_status_t s) {
+  switch (s) {
+    case PA_OK: return "ok";
+    case PA_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case PA_ERR_BAD_SHAPE: return "tensor sizes are inconsistent or out of range";
+    case PA_ERR_BAD_BLOCK_SIZE: return "block_size must divide TILE and be a multiple of 8 (16 for int8)";
+    case PA_ERR_UNSUPPORTED: return "head_dim must be 64, 128 or 256 and x must be 8";
+    case PA_ERR_WORKSPACE: return "workspace is NULL, misaligned or smaller than required";
+    case PA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
+    case PA_ERR_EMPTY_CONTEXT: return "context_lens must be >= 1 (empty sequences unsupported)";
+  }
+  return "unknown status";
+}
+
+const char* pa_version(void) { return "pa_mi355x 0.1 (gfx950)"; }
+
+pa_status_t pa_validate_decode(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                               int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks,
+                               int32_t block_size, int32_t x, int32_t max_blocks_per_seq) {
+  if (kind < PA_DECODE_WARP_F16 || kind > PA_DECODE_SPLITK_I8) return PA_ERR_BAD_SHAPE;
+  // block_size rule of the reference launchers (v3:149-150, v5:167-168).
+  const int mult = is_f16(kind) ? 8 : 16;
+  if (block_size <= 0 || block_size % mult != 0 || kRefTile % block_size != 0)
+    return PA_ERR_BAD_BLOCK_SIZE;
+  if (x != 8) return PA_ERR_UNSUPPORTED;   // int8 rule of v5:176; the fp16 K loads assume it too
+  if (!supported_head_dim(head_dim)) return PA_ERR_UNSUPPORTED;
+  if (num_seqs < 0 || num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0)
+    return PA_ERR_BAD_SHAPE;
+  if (num_seqs > 0 && (num_blocks < 1 || max_blocks_per_seq < 1)) return PA_ERR_BAD_SHAPE;
+  if ((long long)max_blocks_per_seq * block_size > (1LL << 30)) return PA_ERR_BAD_SHAPE;
+  return PA_OK;
+}
+
+pa_status_t pa_check_context_lens(const int32_t* host_context_lens, int32_t num_seqs,
+                                  int32_t* max_len) {
+  if (num_seqs > 0 && !host_context_lens) return PA_ERR_NULL_POINTER;
+  int32_t mx = 0;
+  for (int32_t i = 0; i < num_seqs; ++i) {
+    if (host_context_lens[i] < 1) return PA_ERR_EMPTY_CONTEXT;
+    mx = std::max(mx, host_context_lens[i]);
+  }
+  if (max_len) *max_len = mx;
+  return PA_OK;
+}
+
+pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                           int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                           int32_t max_blocks_per_seq, int32_t max_context_len,
+                           int32_t partition_tokens, int32_t* out_partition_tokens,
+                           int32_t* out_num_splits) {
+  pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads, 1,
+                                      block_size, 8, std::max(1, max_blocks_per_seq));
+  if (st != PA_OK) return st;
+  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, block_size,
+                           std::max(1, max_blocks_per_seq), max_context_len, partition_tokens);
+  if (out_partition_tokens) *out_partition_tokens = p.partition;
+  if (out_num_splits) *out_num_splits = p.nsplit;
+  return PA_OK;
+}
+
+size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                                 int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                                 int32_t max_blocks_per_seq, int32_t max_context_len,
+                                 int32_t partition_tokens) {
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || block_size < 1)
+    return 0;
+  const Plan p = make_plan(kind, std::max(0, num_seqs), num_heads, num_kv_heads, block_size,
+                           std::max(1, max_blocks_per_seq), max_context_len, partition_tokens);
+  return ws_layout(p, head_dim).total;
+}
+
+size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
+  if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) return 0;
+  const int group = num_heads / num_kv_heads;
+  const int units = std::max(0, num_seqs) * num_kv_heads * (group / head_tile_for(group));
+  return align_up((size_t)units * sizeof(uint32_t));
+}
+
+pa_status_t pa_paged_decode_attn_warp(void* out, const void* q, const void* k_cache,
+                                      const void* v_cache, const int32_t* block_table,
+                                      const int32_t* context_lens, float scale,
+                                      int32_t block_size, int32_t num_seqs, int32_t num_heads,
+                                      int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks,
+                                      int32_t x, int32_t max_blocks_per_seq,
+                                      int32_t max_context_len, int32_t partition_tokens,
+                                      void* workspace, size_t workspace_bytes,
+                                      pa_stream_t stream) {
+  return decode_common(PA_DECODE_WARP_F16, out, q, k_cache, v_cache, nullptr, nullptr,
+                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
+                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
+                       partition_tokens, workspace, workspace_bytes, stream);
+}
+
+pa_status_t pa_paged_decode_attn_splitk(void* out, const void* q, const void* k_cache,
+                                        const void* v_cache, const int32_t* block_table,
+                                        const int32_t* context_lens, float scale,
+                                        int32_t block_size, int32_t num_seqs, int32_t num_heads,
+                                        int32_t head_dim, int32_t num_kv_heads,
+                                        int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
+                                        int32_t max_context_len, int32_t partition_tokens,
+                                        void* workspace, size_t workspace_bytes,
+                                        pa_stream_t stream) {
+  return decode_common(PA_DECODE_SPLITK_F16, out, q, k_cache, v_cache, nullptr, nullptr,
+                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
+                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
+                       partition_tokens, workspace, workspace_bytes, stream);
+}
+
+pa_status_t pa_paged_decode_attn_warp_int8(
+    void* out, const void* q, const void* k_cache, const void* v_cache, const float* k_scales,
+    const float* v_scales, const int32_t* block_table, const int32_t* context_lens, float scale,
+    int32_t block_size, int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+    int32_t num_kv_heads, int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
+    int32_t max_context_len, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+    pa_stream_t stream) {
+  return decode_common(PA_DECODE_WARP_I8, out, q, k_cache, v_cache, k_scales, v_scales,
+                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
+                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
+                       partition_tokens, workspace, workspace_bytes, stream);
+}
+
+pa_status_t pa_paged_decode_attn_splitk_int8(
+    void* out, const void* q, const void* k_cache, const void* v_cache, const float* k_scales,
+    const float* v_scales, const int32_t* block_table, const int32_t* context_lens, float scale,
+    int32_t block_size, int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+    int32_t num_kv_heads, int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
+    int32_t max_context_len, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
+    pa_stream_t stream) {
+  return decode_common(PA_DECODE_SPLITK_I8, out, q, k_cache, v_cache, k_scales, v_scales,
+                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
+                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
+                       partition_tokens, workspace, workspace_bytes, stream);
+}
+
+pa_status_t pa_reshape_and_cache_int8(const void* key, const void* value,
+                                      int64_t key_token_stride, int64_t key_head_stride,
+                                      int64_t value_token_stride, int64_t value_head_stride,
+                                      const int64_t* slot_mapping, int32_t num_tokens,
+                                      int32_t num_kv_heads, int32_t head_dim, void* k_cache,
+                                      void* v_cache, float* k_scales, float* v_scales,
+                                      int32_t num_blocks, int32_t block_size, int32_t x,
+                                      pa_stream_t stream) {
+  if (block_size <= 0 || block_size % 16 != 0 || kRefTile % block_size != 0)
+    return PA_ERR_BAD_BLOCK_SIZE;
+  if (x != 8 || !supported_head_dim(head_dim)) return PA_ERR_UNSUPPORTED;
+  if (num_tokens < 0 || num_kv_heads < 1 || num_blocks < 1) return PA_ERR_BAD_SHAPE;
+  if (num_tokens == 0) return PA_OK;
+  if (!key || !value || !slot_mapping || !k_cache || !v_cache || !k_scales || !v_scales)
+    return PA_ERR_NULL_POINTER;
+  // 16-byte row loads and V row stores need 16-byte aligned rows.
+  const int64_t strides[4] = {key_token_stride, key_head_stride, value_token_stride,
+                              value_head_stride};
+  for (int64_t s : strides)
+    if (s < 0 || s % 8 != 0) return PA_ERR_BAD_SHAPE;
+  const void* ptrs[4] = {key, value, k_cache, v_cache};
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return PA_ERR_BAD_SHAPE;
+  pa::QuantLaunch l{};
+  l.key = key;
+  l.value = value;
+  l.key_token_stride = key_token_stride;
+  l.key_head_stride = key_head_stride;
+  l.value_token_stride = value_token_stride;
+  l.value_head_stride = value_head_stride;
+  l.slot_mapping = slot_mapping;
+  l.num_tokens = num_tokens;
+  l.num_kv_heads = num_kv_heads;
+  l.head_dim = head_dim;
+  l.k_cache = k_cache;
+  l.v_cache = v_cache;
+  l.k_scales = k_scales;
+  l.v_scales = v_scales;
+  l.num_blocks = num_blocks;
+  l.block_size = block_size;
+  l.stream = reinterpret_cast<hipStream_t>(stream);
+  return pa::launch_quant_write_i8(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+}
+
+}  // extern "C"

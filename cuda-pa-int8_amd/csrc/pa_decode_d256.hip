@@ -1,0 +1,6 @@
+// Decode kernels instantiated for head_dim = 256 (all head tiles, FP16 and INT8).
+#include "pa_decode_kernels.hpp"
+
+namespace pa {
+hipError_t launch_decode_d256(const DecodeLaunch& l) { return launch_decode_d<256>(l); }
+}  // namespace pa

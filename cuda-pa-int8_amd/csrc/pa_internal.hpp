@@ -1,0 +1,80 @@
+// Launch-level interface between the C ABI (pa_capi.cpp) and the kernel
+// translation units (pa_decode_*.hip, pa_quant.hip).  Host-only types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pa {
+
+constexpr int kWavesPerGroup = 4;    // waves per decode work-group
+constexpr int kIterTokens = 64;      // tokens one wave handles per iteration (4 slabs of 16)
+constexpr int kMaxGroupTile = 8;     // query heads sharing one KV read inside a work-group
+
+// Shape of one decode launch, shared by every decode kernel.
+struct DecodeShape {
+  int num_seqs;
+  int num_heads;
+  int num_kv_heads;
+  int group;        // num_heads / num_kv_heads
+  int nchunk;       // group / head_tile
+  int block_size;
+  int bs_log2;
+  int num_blocks;
+  int max_blocks;   // block_table row stride
+  int partition;    // tokens per split, multiple of kIterTokens
+  int nsplit;       // splits present in the grid
+  int num_items;    // num_seqs * num_kv_heads * nsplit
+  float scale_log2; // softmax scale * log2(e)
+};
+
+struct DecodeLaunch {
+  void* out;
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const float* k_scales;
+  const float* v_scales;
+  const int32_t* block_table;
+  const int32_t* context_lens;
+  float* part_acc;     // [units, nsplit, head_tile, head_dim]
+  float* part_ml;      // [units, nsplit, head_tile, 2]
+  uint32_t* counters;  // [units]
+  int head_dim;
+  int head_tile;
+  bool int8_kv;
+  bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
+  DecodeShape shape;
+  hipStream_t stream;
+};
+
+// Defined in pa_decode_d{64,128,256}.hip.
+hipError_t launch_decode_d64(const DecodeLaunch& l);
+hipError_t launch_decode_d128(const DecodeLaunch& l);
+hipError_t launch_decode_d256(const DecodeLaunch& l);
+
+struct QuantLaunch {
+  const void* key;
+  const void* value;
+  int64_t key_token_stride;
+  int64_t key_head_stride;
+  int64_t value_token_stride;
+  int64_t value_head_stride;
+  const int64_t* slot_mapping;
+  int num_tokens;
+  int num_kv_heads;
+  int head_dim;
+  void* k_cache;
+  void* v_cache;
+  float* k_scales;
+  float* v_scales;
+  int num_blocks;
+  int block_size;
+  hipStream_t stream;
+};
+
+// Defined in pa_quant.hip.
+hipError_t launch_quant_write_i8(const QuantLaunch& l);
+
+}  // namespace pa

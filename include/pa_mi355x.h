@@ -1,0 +1,164 @@
+/*
+ * pa_mi355x.h -- C ABI of the MI355X (gfx950) paged-attention decode path.
+ *
+ * Plain pointers and sizes only: no torch types cross this boundary.  All
+ * device pointers refer to memory on the device that is current when the
+ * call is made; every launch goes to `stream` (a hipStream_t, 0 = the null
+ * stream).  Calls are asynchronous: a PA_OK return means the work was
+ * enqueued, not that it finished.
+ *
+ * Memory layouts (identical to the reference's, kernels/paged_attention_naive.cu:7-9):
+ *   q, out        [num_seqs, num_heads, head_dim]                      fp16
+ *   k_cache       [num_blocks, num_kv_heads, head_dim/x, block_size, x] fp16 or int8, x = 8
+ *   v_cache       [num_blocks, num_kv_heads, head_dim, block_size]      fp16 or int8
+ *   k_scales,
+ *   v_scales      [num_blocks, num_kv_heads, block_size]               fp32 (int8 only)
+ *   block_table   [num_seqs, max_blocks_per_seq]                       int32
+ *   context_lens  [num_seqs]                                           int32
+ * All arrays are dense and row-major.  kv_head of query head h is
+ * h / (num_heads / num_kv_heads).
+ *
+ * Behaviour on data the host cannot see (the caller owns these guarantees;
+ * the kernels stay memory-safe when they are broken):
+ *   - context_lens[s] <= 0 gives out[s] = 0 (the torch shim rejects it first,
+ *     as the reference does);
+ *   - context_lens[s] > max_blocks_per_seq * block_size is clamped to it;
+ *   - a block id outside [0, num_blocks) contributes no tokens.
+ *
+ * Workspace: the decode entry points need device scratch of
+ * pa_decode_workspace_bytes(...) bytes, 256-byte aligned.  Its first
+ * pa_decode_counter_bytes(...) bytes are per-unit arrival counters that must
+ * be zero before the first call; every call leaves them zero again, so a
+ * workspace is zeroed once at allocation and then reused.  Two calls that
+ * may run at the same time (different streams) need different workspaces.
+ */
+#ifndef PA_MI355X_H
+#define PA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pa_stream_t; /* == hipStream_t */
+
+typedef enum pa_status {
+  PA_OK = 0,
+  PA_ERR_NULL_POINTER = 1,     /* a required pointer is NULL */
+  PA_ERR_BAD_SHAPE = 2,        /* sizes inconsistent or out of range */
+  PA_ERR_BAD_BLOCK_SIZE = 3,   /* block_size rejected (same rule as the reference) */
+  PA_ERR_UNSUPPORTED = 4,      /* head_dim / x not built into this library */
+  PA_ERR_WORKSPACE = 5,        /* workspace NULL or smaller than required */
+  PA_ERR_LAUNCH = 6,           /* the HIP runtime refused the launch */
+  PA_ERR_EMPTY_CONTEXT = 7     /* a context length < 1 (host-side check) */
+} pa_status_t;
+
+/* Decode kinds for the planning / workspace queries. */
+typedef enum pa_decode_kind {
+  PA_DECODE_WARP_F16 = 0,
+  PA_DECODE_SPLITK_F16 = 1,
+  PA_DECODE_WARP_I8 = 2,
+  PA_DECODE_SPLITK_I8 = 3
+} pa_decode_kind_t;
+
+const char* pa_status_string(pa_status_t status);
+const char* pa_version(void);
+
+/* Host-only shape validation: the checks the reference launchers make with
+ * TORCH_CHECK (kernels/paged_attention_v3_warp.cu:143-150,
+ * paged_attention_v4_splitk.cu:203-205, paged_attention_v5_warp_int8.cu:159-176),
+ * plus the shape rules of this library.  No device access. */
+pa_status_t pa_validate_decode(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                               int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks,
+                               int32_t block_size, int32_t x, int32_t max_blocks_per_seq);
+
+/* Host-only check of context lengths already copied to the host
+ * (the reference's `context_lens.min().item() >= 1`, paged_attention_v3_warp.cu:147-148).
+ * Writes the maximum to *max_len when max_len != NULL. */
+pa_status_t pa_check_context_lens(const int32_t* host_context_lens, int32_t num_seqs,
+                                  int32_t* max_len);
+
+/* Split plan: how many tokens each work-group covers (a multiple of 64)
+ * and how many splits the longest sequence needs.  `max_context_len` <= 0
+ * means "use max_blocks_per_seq * block_size".  `partition_tokens` > 0
+ * forces the partition size (rounded up to a multiple of 64). */
+pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                           int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                           int32_t max_blocks_per_seq, int32_t max_context_len,
+                           int32_t partition_tokens, int32_t* out_partition_tokens,
+                           int32_t* out_num_splits);
+
+size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                                 int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                                 int32_t max_blocks_per_seq, int32_t max_context_len,
+                                 int32_t partition_tokens);
+size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads);
+
+/* FP16 KV, single launch.  Replaces paged_decode_attn_warp
+ * (kernels/paged_attention_v3_warp.cu:137-176; bound at kernels/bindings.cpp:50-51).
+ * When the (seq, kv-head group) units alone cannot fill the GPU the launch
+ * also splits the context and the last work-group of each unit merges the
+ * partial results in the same launch. */
+pa_status_t pa_paged_decode_attn_warp(
+    void* out, const void* q, const void* k_cache, const void* v_cache,
+    const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
+    int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
+    int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* FP16 KV, split-K: a partition kernel writes per-split (acc, max, sum)
+ * partials and a separate reduce kernel merges them.  Replaces
+ * paged_decode_attn_splitk (kernels/paged_attention_v4_splitk.cu:191-248;
+ * bindings.cpp:52-53). */
+pa_status_t pa_paged_decode_attn_splitk(
+    void* out, const void* q, const void* k_cache, const void* v_cache,
+    const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
+    int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
+    int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* INT8 KV with per-(token, kv_head) fp32 scales, single launch.  Replaces
+ * paged_decode_attn_warp_int8 (kernels/paged_attention_v5_warp_int8.cu:150-197;
+ * bindings.cpp:54-55). */
+pa_status_t pa_paged_decode_attn_warp_int8(
+    void* out, const void* q, const void* k_cache, const void* v_cache,
+    const float* k_scales, const float* v_scales,
+    const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
+    int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
+    int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* INT8 KV, split-K partition + reduce.  Replaces paged_decode_attn_splitk_int8
+ * (kernels/paged_attention_v6_splitk_int8.cu:194-259; bindings.cpp:56-57). */
+pa_status_t pa_paged_decode_attn_splitk_int8(
+    void* out, const void* q, const void* k_cache, const void* v_cache,
+    const float* k_scales, const float* v_scales,
+    const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
+    int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
+    int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+
+/* Per-token INT8 quantize + paged-cache write.  NEW API: the reference has
+ * no kernel for it; its semantics are those of quantize_per_token
+ * (tests/paged_decode_attn.py:106-112) placed as in build_paged_kv_cache_int8
+ * (:190-197) and PagedKVCache.decode_append
+ * (benchmarks/int8_bridge/paged_cache.py:132-156).  Argument convention of
+ * vLLM's reshape_and_cache: key/value [num_tokens, num_kv_heads, head_dim]
+ * fp16 with the given element strides (head_dim stride 1), slot_mapping[t] =
+ * block * block_size + offset; a slot < 0 or >= num_blocks * block_size
+ * skips that token.  Two tokens with the same slot give an unspecified
+ * winner.  block_size must be a multiple of 16 dividing 128; x must be 8. */
+pa_status_t pa_reshape_and_cache_int8(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    void* k_cache, void* v_cache, float* k_scales, float* v_scales,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PA_MI355X_H */
