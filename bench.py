@@ -1,0 +1,436 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 paged-attention decode path on one MI355X.
+
+A step is one decode call over one batch (all sequences, all heads).  The
+headline workload is BASELINE config 2: Qwen2.5-1.5B-shape GQA 12/2,
+head_dim 128, 32 sequences x 4096 tokens, FP16 KV, single-launch kernel.
+``value`` is its algorithmic HBM bytes per step / time per step (GB/s).
+The other BASELINE configs are measured the same way and reported under
+``configs`` (INT8 vs FP16, long-context split-K, ragged serving mix,
+quantize + cache-write, the tiny CPU-runnable case).
+
+Timing: W eager warm-up steps, then the K steps are captured in one HIP
+graph (each step reads a different copy of the cache when one copy would
+fit in the 256 MB Infinity Cache) and replayed once untimed; the timed
+region is one replay of exactly K steps, bracketed by synchronize() and
+HIP events on the stream the kernels run on.  The no-sync entry is timed
+(the reference's ``context_lens.min().item()`` host check is skipped).
+
+    python bench.py [--steps K] [--warmup W] [--configs cfg2,cfg3,...]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(ROOT, "cuda-pa-int8_amd")
+for _p in (ROOT, PKG_ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode µs + achieved HBM GB/s (% of peak), FP16 vs INT8 KV, GQA 12/2 d128"
+MALL_BYTES = 256 << 20
+ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------- inputs
+
+def _block_table(torch, lens, bs, dev, gen):
+    nblk = [(int(n) + bs - 1) // bs for n in lens]
+    nb = sum(nblk) + 1
+    perm = torch.randperm(nb, device=dev, generator=gen).to(torch.int32)
+    bt = torch.zeros((len(lens), max(nblk)), dtype=torch.int32, device=dev)
+    off = 0
+    for s, k in enumerate(nblk):
+        bt[s, :k] = perm[off:off + k]
+        off += k
+    return bt, nb
+
+
+def _randn(torch, shape, dev, gen, outliers):
+    t = torch.randn(shape, dtype=torch.float16, device=dev, generator=gen)
+    if outliers:
+        m = torch.rand(shape, device=dev, generator=gen) < 0.01
+        t = torch.where(m, t * 20, t)
+    return t
+
+
+def make_case(torch, lens, num_heads, num_kv_heads, head_dim, bs, dev, seed, int8, outliers,
+              copies):
+    """Paged caches of N(0,1) fp16 K/V (optionally 1% outliers x20).
+
+    FP16 caches are filled in their layout directly.  INT8 caches are
+    produced by the quantize + write kernel from fp16 tokens, one sequence at
+    a time, so they hold real per-token quantized data.
+    """
+    import pa_int8
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    bt, nb = _block_table(torch, lens, bs, dev, gen)
+    s = len(lens)
+    q = torch.randn((s, num_heads, head_dim), dtype=torch.float16, device=dev, generator=gen)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=dev)
+    caches = []
+    for _ in range(copies):
+        if not int8:
+            kc = _randn(torch, (nb, num_kv_heads, head_dim // 8, bs, 8), dev, gen, outliers)
+            vc = _randn(torch, (nb, num_kv_heads, head_dim, bs), dev, gen, outliers)
+            caches.append((kc, vc, None, None))
+            continue
+        kc = torch.zeros((nb, num_kv_heads, head_dim // 8, bs, 8), dtype=torch.int8, device=dev)
+        vc = torch.zeros((nb, num_kv_heads, head_dim, bs), dtype=torch.int8, device=dev)
+        ks = torch.zeros((nb, num_kv_heads, bs), dtype=torch.float32, device=dev)
+        vs = torch.zeros_like(ks)
+        for si, n in enumerate(lens):
+            t = torch.arange(n, device=dev)
+            slots = bt[si, t // bs].to(torch.int64) * bs + t % bs
+            k = _randn(torch, (n, num_kv_heads, head_dim), dev, gen, outliers)
+            v = _randn(torch, (n, num_kv_heads, head_dim), dev, gen, outliers)
+            pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots)
+        caches.append((kc, vc, ks, vs))
+    torch.cuda.synchronize()
+    return dict(q=q, bt=bt, ctx=ctx, caches=caches, lens=list(lens), bs=bs, nb=nb,
+                scale=1.0 / math.sqrt(head_dim), heads=num_heads, kv_heads=num_kv_heads,
+                head_dim=head_dim)
+
+
+def copies_for(bytes_per_copy):
+    """Enough distinct cache copies that the rotation outruns the Infinity Cache."""
+    return max(1, min(8, math.ceil(2 * MALL_BYTES / max(1, bytes_per_copy))))
+
+
+# --------------------------------------------------------------------------- timing
+
+def time_steps(torch, step_fns, steps, warmup, replays=1):
+    """Median ms per step over `replays` timed graph replays of `steps` steps."""
+    n = len(step_fns)
+    for i in range(warmup):
+        step_fns[i % n]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):            # warm the side stream's workspace
+        for i in range(min(n, 2)):
+            step_fns[i]()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(steps):
+            step_fns[i % n]()
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        with torch.cuda.stream(stream):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            g.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    del g
+    times.sort()
+    return times[len(times) // 2]
+
+
+def time_eager(torch, step_fns, steps):
+    n = len(step_fns)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step_fns[i % n]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def decode_steps(torch, case, variant, partition=0):
+    import pa_int8
+
+    out = torch.empty_like(case["q"])
+    fns = []
+    for kc, vc, ks, vs in case["caches"]:
+        kw = {} if ks is None else dict(k_scales=ks, v_scales=vs)
+
+        def fn(kc=kc, vc=vc, kw=kw):
+            pa_int8.decode(variant, out, case["q"], kc, vc, case["bt"], case["ctx"],
+                           case["scale"], case["bs"], check=False, partition_tokens=partition,
+                           **kw)
+        fns.append(fn)
+    return fns, out
+
+
+# --------------------------------------------------------------------------- configs
+
+def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0, outliers=False,
+                   replays=3, eager=False, partition=0):
+    from pa_int8 import metrics
+
+    int8 = variant.endswith("int8")
+    per_copy = metrics.decode_kv_bytes(lens, hkv, d, 1 if int8 else 2)
+    case = make_case(torch, lens, h, hkv, d, 16, "cuda", seed, int8, outliers,
+                     copies_for(per_copy))
+    fns, _ = decode_steps(torch, case, variant, partition)
+    ms = time_steps(torch, fns, steps, warmup, replays)
+    nbytes = metrics.decode_bytes(lens, h, hkv, d, kv_elem_bytes=1 if int8 else 2, scales=int8)
+    import pa_int8
+
+    part, ns = pa_int8.decode_plan(variant, len(lens), h, d, hkv, 16, case["bt"].shape[1], 0,
+                                   partition)
+    res = dict(variant=variant, us=round(ms * 1e3, 2), algo_bytes=nbytes,
+               gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+               frac_peak=round(nbytes / (ms * 1e-3) / 1e9 / metrics.MI355X_HBM_PEAK_GBS, 4),
+               kv_only_gbs=round(metrics.decode_kv_bytes(lens, hkv, d, 1 if int8 else 2)
+                                 / (ms * 1e-3) / 1e9, 1),
+               seqs=len(lens), heads=f"{h}/{hkv}", head_dim=d, total_tokens=int(sum(lens)),
+               partition_tokens=part, splits=ns, cache_copies=len(case["caches"]),
+               steps=steps)
+    if eager:
+        res["eager_us"] = round(time_eager(torch, fns, steps) * 1e3, 2)
+    del case, fns
+    torch.cuda.empty_cache()
+    log(f"[bench] {name} {variant}: {res['us']} us, {res['gbs']} GB/s "
+        f"({100 * res['frac_peak']:.1f}% of peak)")
+    return res
+
+
+def run_quant_write(torch, steps, warmup, seed=0):
+    import pa_int8
+    from pa_int8 import metrics
+
+    S, L, hkv, d, bs = 64, 8192, 2, 128, 16
+    dev = "cuda"
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    lens = [L] * S
+    bt, nb = _block_table(torch, lens, bs, dev, gen)
+    t = torch.arange(L, device=dev)
+    slots = (bt[:, t // bs].to(torch.int64) * bs + t % bs).reshape(-1)
+    T = S * L
+    k = torch.randn((T, hkv, d), dtype=torch.float16, device=dev, generator=gen)
+    v = torch.randn((T, hkv, d), dtype=torch.float16, device=dev, generator=gen)
+    kc = torch.zeros((nb, hkv, d // 8, bs, 8), dtype=torch.int8, device=dev)
+    vc = torch.zeros((nb, hkv, d, bs), dtype=torch.int8, device=dev)
+    ks = torch.zeros((nb, hkv, bs), dtype=torch.float32, device=dev)
+    vs = torch.zeros_like(ks)
+
+    def fn():
+        pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots)
+
+    ms = time_steps(torch, [fn], steps, warmup, 3)
+    nbytes = metrics.quant_write_bytes(T, hkv, d)
+    res = dict(us=round(ms * 1e3, 2), algo_bytes=nbytes, gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+               frac_peak=round(nbytes / (ms * 1e-3) / 1e9 / metrics.MI355X_HBM_PEAK_GBS, 4),
+               tokens=T, kv_heads=hkv, head_dim=d,
+               slot_pattern="per-sequence block runs (prefill), block ids randomly permuted",
+               steps=steps)
+    log(f"[bench] cfg3w quant_write: {res['us']} us, {res['gbs']} GB/s")
+    del k, v, kc, vc, ks, vs
+    torch.cuda.empty_cache()
+    return res
+
+
+def lognormal_lens(n, seed):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    lens = np.clip(np.round(rng.lognormal(math.log(1024), 1.0, n)), 16, 32768).astype(int)
+    return [int(x) for x in lens]
+
+
+def steps_for(us_est, cap):
+    return int(max(10, min(cap, 40_000 // max(1, us_est))))
+
+
+def run_configs(torch, names, steps, warmup):
+    import numpy as np
+
+    out = {}
+    if "cfg1" in names:
+        rng = np.random.default_rng(0)
+        lens = [int(x) for x in rng.integers(100, 513, size=4)]
+        out["cfg1_tiny_mha_fp16"] = run_decode_cfg(torch, "cfg1", lens, 8, 8, 64, "warp",
+                                                   steps, warmup)
+    if "cfg3" in names:
+        lens = [8192] * 64
+        r8 = run_decode_cfg(torch, "cfg3", lens, 12, 2, 128, "warp_int8", steps_for(40, steps),
+                            warmup)
+        r16 = run_decode_cfg(torch, "cfg3", lens, 12, 2, 128, "warp", steps_for(80, steps),
+                             warmup)
+        out["cfg3_qwen_int8"] = r8
+        out["cfg3_qwen_fp16_same_shape"] = r16
+        out["cfg3_int8_over_fp16_latency"] = round(r8["us"] / r16["us"], 3)
+    if "cfg3w" in names:
+        out["cfg3w_quant_write"] = run_quant_write(torch, steps_for(120, steps), warmup)
+    if "cfg4" in names:
+        for ctx in (32768, 65536, 131072):
+            lens = [ctx] * 8
+            for variant in ("splitk", "splitk_int8"):
+                est = ctx // 250 if variant == "splitk" else ctx // 500
+                out[f"cfg4_llama_{ctx // 1024}k_{variant}"] = run_decode_cfg(
+                    torch, f"cfg4 {ctx}", lens, 32, 8, 128, variant, steps_for(est, steps),
+                    warmup, outliers=True)
+    if "cfg5" in names:
+        lens = lognormal_lens(256, seed=5)
+        for hkv in (8, 1):
+            for variant in ("splitk", "splitk_int8"):
+                out[f"cfg5_ragged_32_{hkv}_{variant}"] = run_decode_cfg(
+                    torch, "cfg5", lens, 32, hkv, 128, variant, steps_for(300, steps), warmup)
+        out["cfg5_lens"] = dict(n=256, median=int(np.median(lens)), mean=float(np.mean(lens)),
+                                max=int(max(lens)), sigma=1.0,
+                                distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
+    return out
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(seconds):
+    """The numpy oracle on config-2-shaped sequences, for a bounded time."""
+    import numpy as np
+
+    from oracle import paged_decode_ref as ref
+    from pa_int8 import metrics
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()
+                       if i.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001
+        threads = 1
+    rng = np.random.default_rng(0)
+    n_seq, ctx, h, hkv, d = 2, 4096, 12, 2, 128
+    lens = np.full(n_seq, ctx, np.int32)
+    nblk = ctx // 16
+    nb = n_seq * nblk + 1
+    kc = rng.standard_normal((nb, hkv, d // 8, 16, 8), dtype=np.float32).astype(np.float16)
+    vc = rng.standard_normal((nb, hkv, d, 16), dtype=np.float32).astype(np.float16)
+    bt = rng.permutation(nb)[:n_seq * nblk].reshape(n_seq, nblk).astype(np.int32)
+    q = rng.standard_normal((n_seq, h, d), dtype=np.float32).astype(np.float16)
+    ref.paged_decode_attention(q, kc, vc, bt, lens, scale=1 / math.sqrt(d))   # warm-up
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ref.paged_decode_attention(q, kc, vc, bt, lens, scale=1 / math.sqrt(d))
+        done += n_seq
+    dt = time.perf_counter() - t0
+    nbytes = metrics.decode_bytes([ctx] * done, h, hkv, d)
+    seq_ms = dt / done * 1e3
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=int(threads),
+                kind="port",
+                sample=(f"numpy oracle (oracle/paged_decode_ref.py) on {done} config-2 sequences "
+                        f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32) in "
+                        f"{dt:.1f} s; {seq_ms:.2f} ms per sequence, "
+                        f"{seq_ms * 32:.1f} ms per 32-sequence step"),
+                host_cpus=os.cpu_count())
+
+
+# --------------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="all",
+                    help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              f"(the decode path runs on a single MI355X; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    import pa_int8
+    from pa_int8 import metrics
+
+    pa_int8.ext()
+    names = ALL_CONFIGS if args.configs == "all" else args.configs.split(",")
+
+    # ---- headline: config 2, single-launch FP16
+    lens = [4096] * 32
+    head = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "warp", args.steps, args.warmup,
+                          replays=1, eager=True)
+    head_sk = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "splitk", args.steps, args.warmup)
+    ms = head["us"] / 1e3
+    nbytes = head["algo_bytes"]
+    achieved = nbytes / (ms * 1e-3) / 1e9
+
+    configs = {"cfg2_qwen_fp16_warp": head, "cfg2_qwen_fp16_splitk": head_sk}
+    configs.update(run_configs(torch, [n for n in names if n != "cfg2"], args.steps,
+                               args.warmup))
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("cfg2_warp_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: fp16 N(0,1) q/K/V, random-permuted block tables, INT8 caches "
+                "quantized from N(0,1) by the write kernel",
+        "config": {
+            "workload": "BASELINE config 2: Qwen2.5-1.5B-shape GQA decode, 12 q / 2 kv heads, "
+                        "head_dim 128, block_size 16, 32 seqs x 4096 ctx, FP16 KV, "
+                        "single-launch kernel (paged_decode_attn_warp)",
+            "seqs": 32, "context": 4096, "heads": "12/2", "head_dim": 128, "block_size": 16,
+            "algo_bytes_per_step": nbytes,
+            "timed_entry": "no host sync (context-length check skipped), HIP graph of K steps",
+            "cache_copies_rotated": head["cache_copies"],
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": metrics.MI355X_HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / metrics.MI355X_HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 
 #include "pa_internal.hpp"
@@ -14,9 +15,14 @@
 namespace {
 
 constexpr int kRefTile = 128;        // reference TILE (paged_attention_v3_warp.cu:20)
-constexpr int kTargetGroups = 1024;  // work-groups one decode launch aims for (256 CUs x 4)
-constexpr int kMinPartition = 256;   // 4 waves x one 64-token iteration
-constexpr int kMaxPartition = 4096;  // caps the serial work of one work-group
+// Split planning, from partition-size sweeps on MI355X (bench configs 2-4):
+// about 2048 resident waves (2 per SIMD with the pipelined loop) in as few
+// splits as possible gave the best times; smaller partitions pay more merge
+// round trips, larger ones leave CUs idle.
+constexpr int kTargetWaves = 2048;   // waves one decode launch aims for (256 CUs x 8)
+constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
+constexpr int kMaxPartition = 4096;  // per 4 waves: caps the serial work of a work-group
+std::atomic<int> g_waves_override{0};
 constexpr size_t kAlign = 256;
 
 bool is_f16(pa_decode_kind_t k) { return k == PA_DECODE_WARP_F16 || k == PA_DECODE_SPLITK_F16; }
@@ -40,18 +46,21 @@ struct Plan {
   int head_tile = 1;
   int nchunk = 1;
   int units = 0;
+  int waves = 4;
   int partition = 0;
   int nsplit = 1;
 };
 
-Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_heads,
-               int block_size, int max_blocks, int max_context_len, int partition_tokens) {
-  (void)kind;
+Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int head_dim, int block_size,
+               int max_blocks, int max_context_len, int partition_tokens) {
   Plan p;
   const int group = num_heads / num_kv_heads;
   p.head_tile = head_tile_for(group);
   p.nchunk = group / p.head_tile;
   p.units = num_seqs * num_kv_heads * p.nchunk;
+  const int ov = g_waves_override.load(std::memory_order_relaxed);
+  p.waves = (ov == 4 || ov == 8) ? ov : 8;
+  if (head_dim > 128) p.waves = 4;     // LDS of the 8-wave merge exceeds 64 KB
   const long long cap = (long long)max_blocks * block_size;
   long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
   if (ctx < 1) ctx = 1;
@@ -60,10 +69,12 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
     part = partition_tokens;
   } else {
     const long long units = std::max(1, p.units);
-    part = (ctx * units + kTargetGroups - 1) / kTargetGroups;
-    part = std::max<long long>(part, kMinPartition);
+    const long long groups = kTargetWaves / p.waves;
+    const long long lo = (long long)kMinPartition * p.waves / 4;
+    const long long hi = (long long)kMaxPartition * p.waves / 4;
+    part = (ctx * units + groups - 1) / groups;
     part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
-    part = std::min<long long>(part, kMaxPartition);
+    part = std::min(std::max(part, lo), hi);
   }
   part = (part + pa::kIterTokens - 1) / pa::kIterTokens * pa::kIterTokens;
   part = std::min<long long>(part, (ctx + pa::kIterTokens - 1) / pa::kIterTokens * pa::kIterTokens);
@@ -99,7 +110,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   if (!out || !q || !k_cache || !v_cache || !block_table || !context_lens) return PA_ERR_NULL_POINTER;
   if (!is_f16(kind) && (!k_scales || !v_scales)) return PA_ERR_NULL_POINTER;
 
-  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, block_size, max_blocks,
+  const Plan p = make_plan(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
                            max_context_len, partition_tokens);
   const WsLayout wl = ws_layout(p, head_dim);
   if (!workspace || workspace_bytes < wl.total) return PA_ERR_WORKSPACE;
@@ -119,7 +130,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.part_ml = reinterpret_cast<float*>(ws + wl.counters);
   l.part_acc = reinterpret_cast<float*>(ws + wl.counters + wl.ml);
   l.head_dim = head_dim;
-  l.head_tile = p.head_tile;
+  l.waves = p.waves;
   l.int8_kv = !is_f16(kind);
   l.fused = is_fused(kind);
   l.stream = reinterpret_cast<hipStream_t>(stream);
@@ -128,6 +139,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   sh.num_heads = num_heads;
   sh.num_kv_heads = num_kv_heads;
   sh.group = num_heads / num_kv_heads;
+  sh.head_tile = p.head_tile;
   sh.nchunk = p.nchunk;
   sh.block_size = block_size;
   sh.bs_log2 = ilog2(block_size);
@@ -204,7 +216,7 @@ pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_
   pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads, 1,
                                       block_size, 8, std::max(1, max_blocks_per_seq));
   if (st != PA_OK) return st;
-  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, block_size,
+  const Plan p = make_plan(num_seqs, num_heads, num_kv_heads, head_dim, block_size,
                            std::max(1, max_blocks_per_seq), max_context_len, partition_tokens);
   if (out_partition_tokens) *out_partition_tokens = p.partition;
   if (out_num_splits) *out_num_splits = p.nsplit;
@@ -217,9 +229,16 @@ size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_
                                  int32_t partition_tokens) {
   if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 || block_size < 1)
     return 0;
-  const Plan p = make_plan(kind, std::max(0, num_seqs), num_heads, num_kv_heads, block_size,
+  (void)kind;
+  const Plan p = make_plan(std::max(0, num_seqs), num_heads, num_kv_heads, head_dim, block_size,
                            std::max(1, max_blocks_per_seq), max_context_len, partition_tokens);
   return ws_layout(p, head_dim).total;
+}
+
+pa_status_t pa_decode_set_waves_per_group(int32_t waves) {
+  if (waves != 0 && waves != 4 && waves != 8) return PA_ERR_BAD_SHAPE;
+  g_waves_override.store(waves, std::memory_order_relaxed);
+  return PA_OK;
 }
 
 size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {

@@ -1,37 +1,43 @@
-// Paged-attention decode kernels for gfx950 (FP16 and INT8 KV).
+// Paged-attention decode kernels for gfx950 (FP16 and INT8 KV), MFMA form.
 //
 // Work decomposition
-//   A work item is (sequence, kv_head, split).  A work-group of 4 waves
-//   serves one work item for a tile of GT query heads of that kv head, so
-//   every K/V byte fetched from HBM feeds GT heads (the reference launches
-//   one block per query head and re-reads KV G times,
-//   kernels/paged_attention_v3_warp.cu:159).  The split's token range is cut
-//   into 64-token iterations dealt round-robin to the 4 waves; each wave
-//   keeps its own online-softmax state and the waves merge through LDS.
+//   A work item is (sequence, kv_head, split).  A work-group of 4 waves serves
+//   one work item for the whole group of query heads that share the kv head
+//   (up to 16), so every K/V byte fetched from HBM feeds all of them (the
+//   reference launches one block per query head and re-reads KV G times,
+//   kernels/paged_attention_v3_warp.cu:159).  The split's tokens are cut into
+//   wave iterations (64 tokens for head_dim <= 128, else 32) dealt round-robin
+//   to the 4 waves; each wave keeps its own online-softmax state and the waves
+//   merge through LDS at the end.
 //
-// Inside one wave iteration (64 tokens = 4 slabs of 16 tokens)
-//   QK: lane l owns token 16*(l>>4) + (l&15) and reads that token's whole K
-//       row: head_dim/8 loads of 16 B (fp16) or 8 B (int8).  The query is
-//       wave-uniform and comes from scalar loads, so no cross-lane reduction
-//       is needed for the dot product (v_dot2: two fp16 MACs per op).
-//   softmax: one wave max per head (DPP + permlane swaps), exp2 with
-//       scale*log2(e) folded in, running (m, l) as in the reference
-//       (paged_attention_v3_warp.cu:84-99).
-//   PV: lane l owns head dims (l>>1) + 32j and the 8 tokens (l&1)*8.. of
-//       each slab, i.e. one 16-B (fp16) / 8-B (int8) load of a V row per
-//       (slab, j); softmax weights come back from LDS as packed fp16.
+// Both products are 16-wide MFMAs (v_mfma_f32_16x16x32_f16):
+//   QK:  S^T[16 token rows][16 heads] += K[rows][32 dims] x Q^T[32 dims][heads]
+//   PV:  O^T[16 dims][16 heads]       += V^T[dims][32 tokens] x P^T[tokens][heads]
+//   Lane l = (r = l & 15, g = l >> 4).  The B operands hold one query head per
+//   lane column, so after QK lane (r, g) owns head r and the scores of the 8
+//   consecutive tokens tok0 + 32p + 8g .. +7 (p = pair of 16-token slabs);
+//   those are exactly the P^T values the same lane feeds to the PV MFMA, and
+//   the PV result O^T lands in the same lane (head r, dims 16t + 4g + e).
+//   Softmax rescaling is therefore lane-local; only the per-head max and sum
+//   are combined over the 4 lanes of a head (permlane swaps).  K rows are
+//   assigned to MFMA rows so that row 4g + e of the first QK MFMA of a pair is
+//   token tok0 + 32p + 8g + e and of the second one token + 4.
+//   The softmax scale is folded into exp2 via scale*log2(e); the running
+//   (max, sum) update is the reference's (paged_attention_v3_warp.cu:84-122).
 //
-// INT8: K is converted to fp16 holding 1152 + k (exact), and the bias is
-//   removed from the dot product with 1152*sum(q); the per-token K scale
-//   multiplies the dot once (paged_attention_v5_warp_int8.cu:80-85).  V is
-//   converted exactly to fp16 integers and its per-token scale is folded into
-//   the softmax weight (v5:99-108) while l accumulates the unscaled weight.
-//   Weights are stored in fp16 multiplied by 2^e with e chosen per iteration
-//   from the largest V scale, so they never overflow fp16 and stay normal.
+// INT8 (paged_attention_v5_warp_int8.cu:80-108 semantics): int8 K and V are
+//   converted to fp16 holding 1152 + value (exact, 3 ops per 4 values); the K
+//   bias is removed from the scores with 1152*sum(q) per head and the V bias
+//   with a packed fp16 subtraction.  s_k multiplies each score; s_v is folded
+//   into the fp16 softmax weight, scaled by 2^e with e chosen per iteration
+//   from the largest s_v so the weights stay normal and below fp16's range;
+//   the running sum l accumulates the unscaled weight.
 //
-// Splits: `fused` (the single-launch warp variant) writes per-split partials
-//   and the last work-group to finish a unit merges them in the same launch;
-//   otherwise (split-K) a separate reduce kernel merges them
+// Splits: FUSED (the single-launch warp variant) writes per-split partials
+//   with device-coherent (write-through) stores, waits for them, counts
+//   arrivals with a device-scope atomic, and the last work-group of a unit
+//   merges with device-coherent loads in the same launch.  Otherwise
+//   (split-K) a separate reduce kernel merges the partials
 //   (paged_attention_v4_splitk.cu:156-187).
 #pragma once
 
@@ -44,58 +50,187 @@
 
 namespace pa {
 
-constexpr int kThreads = kWavesPerGroup * kWave;
+constexpr int kThreads = 4 * kWave;   // split-K reduce work-group
 constexpr float kNegInf = -INFINITY;
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int D, int GT>
-struct alignas(16) DecodeSmem {
-  uint16_t p[kWavesPerGroup][4][GT][16];   // fp16 softmax weights per slab / head / token
-  float m[kWavesPerGroup][GT];
-  float l[kWavesPerGroup][GT];
-  float a[kWavesPerGroup][GT][D];
-  int last;
+__device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Max / sum over the four lanes l, l^16, l^32, l^48 (the lanes of head r).
+__device__ __forceinline__ float head_max(float v) {
+  v = cross_row16(v, OpMax());
+  return cross_half32(v, OpMax());
+}
+__device__ __forceinline__ float head_sum(float v) {
+  v = cross_row16(v, OpSum());
+  return cross_half32(v, OpSum());
+}
+
+// 8 int8 values -> 8 fp16 values holding 1152 + value.
+__device__ __forceinline__ h8_t i8x8_biased(uint2 w) {
+  uint32_t d[4];
+  i8x4_to_biased_h2(w.x, d[0], d[1]);
+  i8x4_to_biased_h2(w.y, d[2], d[3]);
+  return __builtin_bit_cast(h8_t, d);
+}
+// 8 int8 values -> the same values in fp16 (exact).
+__device__ __forceinline__ h8_t i8x8_exact(uint2 w) {
+  uint32_t d[4];
+  i8x4_to_biased_h2(w.x, d[0], d[1]);
+  i8x4_to_biased_h2(w.y, d[2], d[3]);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) d[k] = unbias_h2(d[k]);
+  return __builtin_bit_cast(h8_t, d);
+}
+
+// Zero the fp16 elements e >= n of an 8-element row (tokens past the end may
+// hold NaN bits, and 0 * NaN would poison the PV product).
+__device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
+  uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t m = (2 * k + 1 < n) ? 0xFFFFFFFFu : ((2 * k < n) ? 0x0000FFFFu : 0u);
+    d[k] &= m;
+  }
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// LDS of the split merge: weights of up to 64 splits at a time, per head.
+struct MergeSmem {
+  float w[64][16];
+  float inv_l[16];
 };
 
-// Merge `ns` split partials of one unit and write the fp16 output rows.
-template <int D, int GT>
+// Merge the `ns` partials of one unit (gt heads) and write its fp16 output
+// rows.  Partials: acc[gt][D] (relative to m), then (m, l) per split and head.
+// COHERENT: read with device-coherent loads (partials written in this launch).
+// Loads are issued in independent batches so the merge costs a few memory
+// round trips, not one per split.  Called by every thread of the work-group.
+template <int D, int THREADS, bool COHERENT>
 __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
-                                               const float* __restrict__ pml, half_t* __restrict__ out,
-                                               size_t part_base, size_t out_base, int ns) {
-  for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
-    const int hh = idx / D;
-    const int d = idx - hh * D;
-    float mx = kNegInf;
-    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, pml[((part_base + s) * GT + hh) * 2]);
-    float a = 0.f, l = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const size_t pi = (part_base + s) * GT + hh;
-      const float ms = pml[pi * 2];
-      const float f = (ms == kNegInf) ? 0.f : exp2f_fast(ms - mx);
-      l += pml[pi * 2 + 1] * f;
-      a += pacc[pi * D + d] * f;
+                                               const float* __restrict__ pml,
+                                               half_t* __restrict__ out, size_t part_base, int gt,
+                                               size_t out_base, int ns, MergeSmem& msm) {
+  constexpr int PER = (16 * D + THREADS - 1) / THREADS;
+  constexpr int SB = 4;   // splits per batch of accumulator loads
+  auto ld = [](const float* p) -> float {
+    if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+  };
+  const int tid = threadIdx.x;
+  // Per head h: 16 threads (one DPP row) own the splits k, k+16, k+32, ...
+  const int h = tid >> 4, k = tid & 15;
+  const bool hv = h < gt;
+  float mv[4], lv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int sp = k + 16 * u;
+    const bool ok = hv && sp < ns;
+    const size_t pi = (part_base + sp) * gt + h;
+    mv[u] = ok ? ld(pml + pi * 2) : kNegInf;
+    lv[u] = ok ? ld(pml + pi * 2 + 1) : 0.f;
+  }
+  float mx = kNegInf;
+  for (int sp = k + 64; hv && sp < ns; sp += 16) mx = fmaxf(mx, ld(pml + ((part_base + sp) * gt + h) * 2));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) mx = fmaxf(mx, mv[u]);
+  mx = fmaxf(mx, dpp_mov<kQuadXor1>(mx));
+  mx = fmaxf(mx, dpp_mov<kQuadXor2>(mx));
+  mx = fmaxf(mx, dpp_mov<kRowHalfMirror>(mx));
+  mx = fmaxf(mx, dpp_mov<kRowMirror>(mx));
+  float l = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) l += mv[u] == kNegInf ? 0.f : lv[u] * exp2f_fast(mv[u] - mx);
+  for (int sp = k + 64; hv && sp < ns; sp += 16) {
+    const size_t pi = (part_base + sp) * gt + h;
+    const float m_s = ld(pml + pi * 2);
+    if (m_s != kNegInf) l += ld(pml + pi * 2 + 1) * exp2f_fast(m_s - mx);
+  }
+  l += dpp_mov<kQuadXor1>(l);
+  l += dpp_mov<kQuadXor2>(l);
+  l += dpp_mov<kRowHalfMirror>(l);
+  l += dpp_mov<kRowMirror>(l);
+  if (k == 0 && hv) msm.inv_l[h] = l > 0.f ? 1.f / l : 0.f;
+  float a[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) a[i] = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    const int se = min(ns, s0 + 64);
+    __syncthreads();
+    if (s0 == 0) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (hv && k + 16 * u < ns) msm.w[k + 16 * u][h] = mv[u] == kNegInf ? 0.f : exp2f_fast(mv[u] - mx);
+    } else if (hv) {
+      for (int sp = s0 + k; sp < se; sp += 16) {
+        const float m_s = ld(pml + ((part_base + sp) * gt + h) * 2);
+        msm.w[sp - s0][h] = m_s == kNegInf ? 0.f : exp2f_fast(m_s - mx);
+      }
     }
-    out[out_base + (size_t)hh * D + d] = (half_t)(l > 0.f ? a / l : 0.f);
+    __syncthreads();
+    for (int sb = s0; sb < se; sb += SB) {
+      float v[SB][PER];
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int idx = tid + i * THREADS;
+          const int hh = idx / D, d = idx - hh * D;
+          const int sp = sb + u;
+          v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((part_base + sp) * gt + hh) * D + d) : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int hh = (tid + i * THREADS) / D;
+          const int sp = sb + u;
+          if (sp < se && hh < gt) a[i] += v[u][i] * msm.w[sp - s0][hh];
+        }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = tid + i * THREADS;
+    const int hh = idx / D, d = idx - hh * D;
+    if (hh < gt) out[out_base + (size_t)hh * D + d] = (half_t)(a[i] * msm.inv_l[hh]);
   }
 }
 
-template <int D, int GT, bool I8, bool FUSED>
-__global__ void __launch_bounds__(kThreads)
+template <int D, int NW>
+struct alignas(16) DecodeSmem {
+  float a[NW / 2][16][D];   // merge slots: per head, per dim
+  float m[NW / 2][16];
+  float l[NW / 2][16];
+  int last;
+  MergeSmem merge;
+};
+
+template <int D, int NW, bool I8, bool FUSED>
+__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
               const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
               const float* __restrict__ vsc, const int* __restrict__ bt,
               const int* __restrict__ ctxl, half_t* __restrict__ out, float* __restrict__ pacc,
               float* __restrict__ pml, uint32_t* __restrict__ cnt, DecodeShape sh) {
-  constexpr int NO = D / 8;         // K groups of 8 dims per token
-  constexpr int JV = D / 32;        // V rows per lane per slab
-  constexpr int ESZ = I8 ? 1 : 2;   // bytes per cache element
-  constexpr bool VEARLY = D <= 128; // issue all V loads before the QK math
-  using KVec = typename std::conditional<I8, uint2, uint4>::type;
+  constexpr int KC = D / 32;                 // 32-dim k-chunks of one QK product
+  constexpr int NT = D / 16;                 // 16-dim output tiles of PV
+  constexpr int PAIRS = D <= 128 ? 2 : 1;    // 32-token pairs per wave iteration
+  constexpr int IT = 32 * PAIRS;             // tokens per wave iteration
+  constexpr int ESZ = I8 ? 1 : 2;            // bytes per cache element
+  using LVec = typename std::conditional<I8, uint2, uint4>::type;   // 8 elements
 
-  __shared__ DecodeSmem<D, GT> sm;
+  static_assert(sizeof(DecodeSmem<D, NW>) <= 64 * 1024, "LDS budget");
+  __shared__ DecodeSmem<D, NW> sm;
 
-  // ---- work item (XCD-aware: the head tiles of one item share blockIdx % 8)
+  // ---- work item (XCD-aware: the head chunks of one item share blockIdx % 8)
   const int wg = blockIdx.x;
   const int per_grp = 8 * sh.nchunk;
   const int grp = wg / per_grp;
@@ -107,6 +242,7 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   const int sk = item / sh.nsplit;
   const int kvh = sk % sh.num_kv_heads;
   const int seq = sk / sh.num_kv_heads;
+  const int gt = sh.head_tile;
 
   // Contexts are clamped to what the block table holds and to what the grid's
   // splits cover, so no work-group reads past the table or the partials.
@@ -117,278 +253,344 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   if (split >= ns_eff) return;
   const int t_begin = split * sh.partition;
   const int t_end = min(ctx, t_begin + sh.partition);
-  const int n_it = t_end > t_begin ? (t_end - t_begin + kIterTokens - 1) / kIterTokens : 0;
+  const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int head0 = kvh * sh.group + chunk * GT;
+  const int r = lane & 15, g = lane >> 4;
+  const int head0 = kvh * sh.group + chunk * gt;
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
-
-  const uint32_t* q32 =
-      reinterpret_cast<const uint32_t*>(q + ((size_t)seq * sh.num_heads + head0) * D);
   const int* btrow = bt + (size_t)seq * sh.max_blocks;
-  const int bs = sh.block_size;
-  const int bsl = sh.bs_log2;
+  const int bs = sh.block_size, bsl = sh.bs_log2;
+  const int hkv = sh.num_kv_heads;
 
-  // 1152 * sum(q) per head, removes the fp16 bias of the converted int8 K.
-  float qbias[GT];
-  if constexpr (I8) {
+  // ---- query operand: lane (r, g) holds q[head r][32kk + 8g .. +7]
+  h8_t qreg[KC];
+  {
+    const bool hv = r < gt;
+    const half_t* qrow = q + ((size_t)seq * sh.num_heads + head0 + (hv ? r : 0)) * D + 8 * g;
 #pragma unroll
-    for (int hh = 0; hh < GT; ++hh) {
-      float sacc = 0.f;
-      for (int i = lane; i < D / 2; i += kWave) sacc = dot2(q32[hh * (D / 2) + i], 0x3C003C00u, sacc);
-      qbias[hh] = 1152.f * wave_sum(sacc);
+    for (int kk = 0; kk < KC; ++kk) {
+      const uint4 v = hv ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
+      qreg[kk] = __builtin_bit_cast(h8_t, v);
     }
   }
-
-  float m_run[GT], l_run[GT], acc[GT][JV];
+  float qbias = 0.f;
+  if constexpr (I8) {
+    float s = 0.f;
 #pragma unroll
-  for (int hh = 0; hh < GT; ++hh) {
-    m_run[hh] = kNegInf;
-    l_run[hh] = 0.f;
-#pragma unroll
-    for (int j = 0; j < JV; ++j) acc[hh][j] = 0.f;
+    for (int kk = 0; kk < KC; ++kk) {
+      const uint4 v = __builtin_bit_cast(uint4, qreg[kk]);
+      s = dot2(v.x, 0x3C003C00u, s);
+      s = dot2(v.y, 0x3C003C00u, s);
+      s = dot2(v.z, 0x3C003C00u, s);
+      s = dot2(v.w, 0x3C003C00u, s);
+    }
+    qbias = 1152.f * head_sum(s);
   }
-  int e_cur = I8 ? 0 : 14;
 
-  const int kb = lane >> 4, kt = lane & 15;   // QK lane: slab, token
-  const int vd = lane >> 1, vh = lane & 1;    // PV lane: dim row, token half
+  float m_run = kNegInf, l_part = 0.f;
+  f4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+  int e_cur = I8 ? 0 : 14;
   const float c = sh.scale_log2;
 
-  for (int it = w; it < n_it; it += kWavesPerGroup) {
-    const int tok0 = t_begin + it * kIterTokens;
+  // ---- software-pipelined token loop.  In iteration `it` the block ids of
+  // the wave's next iteration are loaded first; its K rows are issued as soon
+  // as the QK MFMAs have consumed this iteration's K registers, and its V rows
+  // (plus INT8 scales) as soon as the PV MFMAs have consumed the V registers,
+  // so HBM traffic of the next iteration overlaps this iteration's math.
+  struct Blocks {
+    int kb[PAIRS];
+    int vb[PAIRS];
+  };
+  LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
+  float ksv[PAIRS][8], vsv[PAIRS][8];   // INT8 scales of this lane's 8 tokens
+  int nvalid[PAIRS];                    // valid tokens among this lane's 8
 
-    // ---- K addressing and loads (one token per lane)
-    const int tau = tok0 + kb * 16 + kt;
-    bool vk = tau < t_end;
-    const int tau_c = vk ? tau : t_begin;
-    int blk = btrow[tau_c >> bsl];
-    const int off = tau_c & (bs - 1);
-    const bool bok = (unsigned)blk < (unsigned)sh.num_blocks;
-    vk = vk && bok;
-    blk = bok ? blk : 0;
-    const size_t kslot = (size_t)blk * sh.num_kv_heads + kvh;
-    const uint8_t* kp = kc + (kslot * NO * bs + off) * 8 * ESZ;
-    KVec kr[NO];
+  auto load_blocks = [&](int it_, Blocks& b) {
+    const int tok0 = t_begin + it_ * IT;
 #pragma unroll
-    for (int o = 0; o < NO; ++o) kr[o] = *reinterpret_cast<const KVec*>(kp + (size_t)o * bs * 8 * ESZ);
-
-    float sk = 1.f, sv = 0.f;
-    if constexpr (I8) {
-      sk = ksc[kslot * bs + off];
-      sv = vsc[kslot * bs + off];
+    for (int p = 0; p < PAIRS; ++p) {
+      const int kg = tok0 + 32 * p + 8 * (r >> 2);
+      const int tg = tok0 + 32 * p + 8 * g;
+      b.kb[p] = btrow[(kg < t_end ? kg : t_begin) >> bsl];
+      b.vb[p] = btrow[(tg < t_end ? tg : t_begin) >> bsl];
     }
-
-    // ---- V addressing (8 tokens x JV rows per lane and slab)
-    const uint8_t* vp[4];
-    int nval[4];
+  };
+  // K rows: token tok0 + 32p + 8(r>>2) + (r&3) (first MFMA) and + 4 (second).
+  auto issue_k = [&](int it_, const Blocks& b) {
+    const int tok0 = t_begin + it_ * IT;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int tv = tok0 + b * 16 + vh * 8;
-      const bool in = tv < t_end;
-      const int tv_c = in ? tv : t_begin;
-      int vb = btrow[tv_c >> bsl];
-      const int voff = tv_c & (bs - 1);
-      const bool vok = (unsigned)vb < (unsigned)sh.num_blocks;
-      vb = vok ? vb : 0;
-      vp[b] = vc + ((((size_t)vb * sh.num_kv_heads + kvh) * D + vd) * bs + voff) * ESZ;
-      const int nv = t_end - tv;
-      nval[b] = (in && vok) ? (nv < 8 ? nv : 8) : 0;
+    for (int p = 0; p < PAIRS; ++p) {
+      const int kg = tok0 + 32 * p + 8 * (r >> 2);
+      const int kgc = kg < t_end ? kg : t_begin;
+      const int kb = (unsigned)b.kb[p] < (unsigned)sh.num_blocks ? b.kb[p] : 0;
+      const int koff = (kgc & (bs - 1)) + (r & 3);
+      const uint8_t* kp = kc + ((((size_t)kb * hkv + kvh) * (D / 8) + g) * bs + koff) * 8 * ESZ;
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        const uint8_t* p0 = kp + (size_t)(4 * kk) * bs * 8 * ESZ;
+        kx[p][kk] = *reinterpret_cast<const LVec*>(p0);
+        ky[p][kk] = *reinterpret_cast<const LVec*>(p0 + 4 * 8 * ESZ);
+      }
     }
-    KVec vr[VEARLY ? 4 : 1][JV];
-    if constexpr (VEARLY) {
+  };
+  // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7.
+  auto issue_v = [&](int it_, const Blocks& b) {
+    const int tok0 = t_begin + it_ * IT;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+    for (int p = 0; p < PAIRS; ++p) {
+      const int tg = tok0 + 32 * p + 8 * g;
+      const bool tin = tg < t_end;
+      const int tgc = tin ? tg : t_begin;
+      const bool vok = (unsigned)b.vb[p] < (unsigned)sh.num_blocks;
+      const int vb = vok ? b.vb[p] : 0;
+      const int voff = tgc & (bs - 1);
+      nvalid[p] = (tin && vok) ? min(8, t_end - tg) : 0;
+      const size_t slot = ((size_t)vb * hkv + kvh) * bs + voff;
+      const uint8_t* vp = vc + ((((size_t)vb * hkv + kvh) * D + r) * bs + voff) * ESZ;
 #pragma unroll
-        for (int j = 0; j < JV; ++j)
-          vr[b][j] = *reinterpret_cast<const KVec*>(vp[b] + (size_t)j * 32 * bs * ESZ);
-    }
-
-    // ---- QK: q from scalar loads (re-read every iteration from the scalar cache)
-    uint32_t zo;
-    asm volatile("s_mov_b32 %0, 0" : "=s"(zo));
-    const uint32_t* qq = q32 + zo;
-    float s[GT];
-#pragma unroll
-    for (int hh = 0; hh < GT; ++hh) s[hh] = 0.f;
-#pragma unroll
-    for (int o = 0; o < NO; ++o) {
-      uint32_t k0, k1, k2, k3;
+      for (int t = 0; t < NT; ++t)
+        vr[p][t] = *reinterpret_cast<const LVec*>(vp + (size_t)(16 * t) * bs * ESZ);
       if constexpr (I8) {
-        i8x4_to_biased_h2(kr[o].x, k0, k1);
-        i8x4_to_biased_h2(kr[o].y, k2, k3);
-      } else {
-        k0 = kr[o].x; k1 = kr[o].y; k2 = kr[o].z; k3 = kr[o].w;
-      }
-#pragma unroll
-      for (int hh = 0; hh < GT; ++hh) {
-        const uint4 qv = *reinterpret_cast<const uint4*>(qq + hh * (D / 2) + o * 4);
-        float t = dot2(qv.x, k0, s[hh]);
-        t = dot2(qv.y, k1, t);
-        t = dot2(qv.z, k2, t);
-        s[hh] = dot2(qv.w, k3, t);
+        const float4 a0 = *reinterpret_cast<const float4*>(ksc + slot);
+        const float4 a1 = *reinterpret_cast<const float4*>(ksc + slot + 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(vsc + slot);
+        const float4 b1 = *reinterpret_cast<const float4*>(vsc + slot + 4);
+        ksv[p][0] = a0.x; ksv[p][1] = a0.y; ksv[p][2] = a0.z; ksv[p][3] = a0.w;
+        ksv[p][4] = a1.x; ksv[p][5] = a1.y; ksv[p][6] = a1.z; ksv[p][7] = a1.w;
+        vsv[p][0] = b0.x; vsv[p][1] = b0.y; vsv[p][2] = b0.z; vsv[p][3] = b0.w;
+        vsv[p][4] = b1.x; vsv[p][5] = b1.y; vsv[p][6] = b1.z; vsv[p][7] = b1.w;
       }
     }
+  };
 
-    // ---- online softmax, one wave max per head
-    float p[GT], fac[GT];
-    const float skc = sk * c;
+  if (w < n_it) {
+    Blocks b0;
+    load_blocks(w, b0);
+    issue_k(w, b0);
+    issue_v(w, b0);
+  }
+  for (int it = w; it < n_it; it += NW) {
+    const bool has_next = it + NW < n_it;
+    Blocks bn;
+    if (has_next) load_blocks(it + NW, bn);
+    // Tokens past the end or in invalid blocks exist only in the last
+    // iteration of a split (or with a corrupt block table): mask only then.
+    const bool need_mask =
+        __builtin_amdgcn_ballot_w64(nvalid[0] < 8 || nvalid[PAIRS - 1] < 8) != 0;
+
+    // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r
+    float s[PAIRS][8];
 #pragma unroll
-    for (int hh = 0; hh < GT; ++hh) {
-      float sc;
-      if constexpr (I8) sc = (s[hh] - qbias[hh]) * skc;
-      else sc = s[hh] * c;
-      sc = vk ? sc : kNegInf;
-      const float mt = wave_max(sc);
-      const float m_new = fmaxf(m_run[hh], mt);
-      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-      fac[hh] = exp2f_fast(m_run[hh] - m_use);
-      p[hh] = exp2f_fast(sc - m_use);
-      l_run[hh] = l_run[hh] * fac[hh] + p[hh];
-      m_run[hh] = m_new;
+    for (int p = 0; p < PAIRS; ++p) {
+      f4_t sx = {0.f, 0.f, 0.f, 0.f}, sy = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        h8_t ax, ay;
+        if constexpr (I8) {
+          ax = i8x8_biased(kx[p][kk]);
+          ay = i8x8_biased(ky[p][kk]);
+        } else {
+          ax = __builtin_bit_cast(h8_t, kx[p][kk]);
+          ay = __builtin_bit_cast(h8_t, ky[p][kk]);
+        }
+        sx = mfma16(ax, qreg[kk], sx);
+        sy = mfma16(ay, qreg[kk], sy);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[p][e] = sx[e];
+        s[p][4 + e] = sy[e];
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) issue_k(it + NW, bn);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- weights to fp16 (times 2^e) into LDS
-    float wscale;
+    // ---- online softmax (lane-local except the per-head max)
+    float mloc = kNegInf;
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v;
+        if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
+        else v = s[p][j] * c;
+        s[p][j] = v;
+      }
+    if (need_mask) {
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          s[p][j] = j < nvalid[p] ? s[p][j] : kNegInf;
+          if constexpr (I8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mloc = fmaxf(mloc, s[p][j]);
+    const float m_new = fmaxf(m_run, head_max(mloc));
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha_m = exp2f_fast(m_run - m_use);   // rescales l
+    float alpha_acc = alpha_m;                         // rescales acc (incl. weight exponent)
+    m_run = m_new;
+    float wsc;
     if constexpr (I8) {
-      const float svm = vk ? sv : 0.f;
-      const float msv = wave_max(svm);
-      int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
-      e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
-      wscale = __builtin_amdgcn_ldexpf(svm, e_new);
+      float msv = 0.f;
 #pragma unroll
-      for (int hh = 0; hh < GT; ++hh) fac[hh] = __builtin_amdgcn_ldexpf(fac[hh], e_new - e_cur);
-      e_cur = e_new;
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
+      // Every head's lanes see the same tokens, so this max is wave-uniform.
+      msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
+      // Keep the weight exponent while the largest weight stays in [2^12, 2^15).
+      const float top = __builtin_amdgcn_ldexpf(msv, e_cur);
+      if (msv > 0.f && (top >= 32768.f || top < 4096.f)) {
+        int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
+        e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
+        alpha_acc = __builtin_amdgcn_ldexpf(alpha_m, e_new - e_cur);
+        e_cur = e_new;
+      }
+      wsc = __builtin_amdgcn_ldexpf(1.f, e_cur);
     } else {
-      wscale = 16384.f;
+      wsc = 16384.f;
     }
+    float lsum = 0.f;
+    h8_t pb[PAIRS];
 #pragma unroll
-    for (int hh = 0; hh < GT; ++hh) {
-      const half_t ph = (half_t)(p[hh] * wscale);
-      sm.p[w][kb][hh][kt] = __builtin_bit_cast(uint16_t, ph);
+    for (int p = 0; p < PAIRS; ++p) {
 #pragma unroll
-      for (int j = 0; j < JV; ++j) acc[hh][j] *= fac[hh];
+      for (int j = 0; j < 8; ++j) {
+        const float pj = exp2f_fast(s[p][j] - m_use);
+        lsum += pj;
+        float wj;
+        if constexpr (I8) wj = pj * vsv[p][j] * wsc;
+        else wj = pj * wsc;
+        pb[p][j] = (half_t)wj;
+      }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    l_part = l_part * alpha_m + lsum;
+    if (__builtin_amdgcn_ballot_w64(alpha_acc != 1.f) != 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] *= alpha_acc;
+    }
 
     // ---- PV
-    const bool need_mask = !I8 && (__builtin_amdgcn_ballot_w64(nval[0] < 8 || nval[1] < 8 ||
-                                                               nval[2] < 8 || nval[3] < 8) != 0);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      KVec vraw[JV];
+    for (int p = 0; p < PAIRS; ++p) {
 #pragma unroll
-      for (int j = 0; j < JV; ++j) {
-        if constexpr (VEARLY) vraw[j] = vr[b][j];
-        else vraw[j] = *reinterpret_cast<const KVec*>(vp[b] + (size_t)j * 32 * bs * ESZ);
-      }
-      uint32_t vv[JV][4];
-#pragma unroll
-      for (int j = 0; j < JV; ++j) {
+      for (int t = 0; t < NT; ++t) {
+        h8_t av;
         if constexpr (I8) {
-          i8x4_to_biased_h2(vraw[j].x, vv[j][0], vv[j][1]);
-          i8x4_to_biased_h2(vraw[j].y, vv[j][2], vv[j][3]);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) vv[j][k] = unbias_h2(vv[j][k]);
+          av = i8x8_exact(vr[p][t]);
         } else {
-          vv[j][0] = vraw[j].x; vv[j][1] = vraw[j].y; vv[j][2] = vraw[j].z; vv[j][3] = vraw[j].w;
+          uint4 v = vr[p][t];
+          if (need_mask) v = keep_first(v, nvalid[p]);
+          av = __builtin_bit_cast(h8_t, v);
         }
-      }
-      if (need_mask) {
-        // Zero the fp16 V of tokens past the end (they may hold NaN bits).
-        const int n = nval[b];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t mk = (2 * k + 1 < n) ? 0xFFFFFFFFu : ((2 * k < n) ? 0x0000FFFFu : 0u);
-#pragma unroll
-          for (int j = 0; j < JV; ++j) vv[j][k] &= mk;
-        }
-      }
-#pragma unroll
-      for (int hh = 0; hh < GT; ++hh) {
-        const uint4 pp = *reinterpret_cast<const uint4*>(&sm.p[w][b][hh][vh * 8]);
-#pragma unroll
-        for (int j = 0; j < JV; ++j) {
-          float t = dot2(pp.x, vv[j][0], acc[hh][j]);
-          t = dot2(pp.y, vv[j][1], t);
-          t = dot2(pp.z, vv[j][2], t);
-          acc[hh][j] = dot2(pp.w, vv[j][3], t);
-        }
+        acc[t] = mfma16(av, pb[p], acc[t]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) issue_v(it + NW, bn);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // ---- per-wave results
+  // ---- per-wave results: m (head r), l, acc (dims 16t + 4g + e)
+  float l_run = head_sum(l_part);
   const float unscale = __builtin_amdgcn_ldexpf(1.f, -e_cur);
 #pragma unroll
-  for (int hh = 0; hh < GT; ++hh) {
-    l_run[hh] = wave_sum(l_run[hh]);
-#pragma unroll
-    for (int j = 0; j < JV; ++j) acc[hh][j] = pair_sum(acc[hh][j]) * unscale;
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int hh = 0; hh < GT; ++hh) {
-      sm.m[w][hh] = m_run[hh];
-      sm.l[w][hh] = l_run[hh];
-    }
-  }
-  if ((lane & 1) == 0) {
-#pragma unroll
-    for (int hh = 0; hh < GT; ++hh)
-#pragma unroll
-      for (int j = 0; j < JV; ++j) sm.a[w][hh][vd + 32 * j] = acc[hh][j];
-  }
-  __syncthreads();
+  for (int t = 0; t < NT; ++t) acc[t] *= unscale;
 
-  // ---- merge the 4 waves
-  const bool final_here = FUSED && ns_eff == 1;
+  // ---- merge the NW waves pairwise through LDS: [NW/2, NW) -> [0, NW/2), ...
+#pragma unroll
+  for (int half = NW / 2; half >= 1; half /= 2) {
+    if (w >= half && w < 2 * half) {
+      const int slot = w - half;
+      if (g == 0) {
+        sm.m[slot][r] = m_run;
+        sm.l[slot][r] = l_run;
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        *reinterpret_cast<f4_t*>(&sm.a[slot][r][16 * t + 4 * g]) = acc[t];
+    }
+    __syncthreads();
+    if (w < half) {
+      const float m2 = sm.m[w][r], l2 = sm.l[w][r];
+      const float mx = fmaxf(m_run, m2);
+      const float f1 = m_run == kNegInf ? 0.f : exp2f_fast(m_run - mx);
+      const float f2 = m2 == kNegInf ? 0.f : exp2f_fast(m2 - mx);
+      l_run = l_run * f1 + l2 * f2;
+      m_run = mx;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t] = acc[t] * f1 + *reinterpret_cast<const f4_t*>(&sm.a[w][r][16 * t + 4 * g]) * f2;
+    }
+    __syncthreads();
+  }
+
+  // ---- wave 0 holds the work-group result
   const size_t out_base = ((size_t)seq * sh.num_heads + head0) * D;
   const size_t part_base = (size_t)unit * sh.nsplit;
-  for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
-    const int hh = idx / D;
-    const int d = idx - hh * D;
-    float mx = kNegInf;
-#pragma unroll
-    for (int ww = 0; ww < kWavesPerGroup; ++ww) mx = fmaxf(mx, sm.m[ww][hh]);
-    float a = 0.f, l = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < kWavesPerGroup; ++ww) {
-      const float mw = sm.m[ww][hh];
-      const float f = (mw == kNegInf) ? 0.f : exp2f_fast(mw - mx);
-      a += sm.a[ww][hh][d] * f;
-      l += sm.l[ww][hh] * f;
-    }
+  const bool final_here = FUSED && ns_eff == 1;
+  if (w == 0 && r < gt) {
     if (final_here) {
-      out[out_base + idx] = (half_t)(l > 0.f ? a / l : 0.f);
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f4_t v = acc[t] * inv;
+        const uint2 pk = make_uint2(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]));
+        *reinterpret_cast<uint2*>(out + out_base + (size_t)r * D + 16 * t + 4 * g) = pk;
+      }
     } else {
-      const size_t pi = (part_base + split) * GT + hh;
-      pacc[pi * D + d] = a;
-      if (d == 0) {
-        pml[pi * 2] = mx;
-        pml[pi * 2 + 1] = l;
+      const size_t pi = (part_base + split) * gt + r;
+      float* pa = pacc + pi * D + 4 * g;
+      if constexpr (FUSED) {
+        // Device-coherent (write-through) stores: visible to every XCD once
+        // this thread's stores are acknowledged.
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            __hip_atomic_store(pa + 16 * t + e, acc[t][e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (g == 0) {
+          __hip_atomic_store(pml + pi * 2, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(pml + pi * 2 + 1, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) *reinterpret_cast<f4_t*>(pa + 16 * t) = acc[t];
+        if (g == 0) {
+          pml[pi * 2] = m_run;
+          pml[pi * 2 + 1] = l_run;
+        }
       }
     }
   }
   if constexpr (FUSED) {
     if (ns_eff > 1) {
-      // Release this split's partial, count arrivals; the last one merges.
-      __threadfence();
+      // Wait until this thread's partial stores are acknowledged, then count
+      // the arrival; the last work-group of the unit merges every split.
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       __syncthreads();
       if (threadIdx.x == 0) {
         const uint32_t prev =
-            __hip_atomic_fetch_add(cnt + unit, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sm.last = prev == (uint32_t)(ns_eff - 1);
       }
       __syncthreads();
       if (sm.last) {
-        __threadfence();
-        merge_partials<D, GT>(pacc, pml, out, part_base, out_base, ns_eff);
+        merge_partials<D, NW * kWave, true>(pacc, pml, out, part_base, gt, out_base, ns_eff,
+                                            sm.merge);
         if (threadIdx.x == 0)
           __hip_atomic_store(cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -396,29 +598,28 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   }
 }
 
-// Split-K reduce: one work-group per (seq, kv_head, head tile).
-template <int D, int GT>
+// Split-K reduce: one work-group per (seq, kv_head, head chunk).
+template <int D>
 __global__ void __launch_bounds__(kThreads)
 splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
                      const int* __restrict__ ctxl, half_t* __restrict__ out, DecodeShape sh) {
+  __shared__ MergeSmem msm;
   const int unit = blockIdx.x;
   const int chunk = unit % sh.nchunk;
   const int sk = unit / sh.nchunk;
   const int kvh = sk % sh.num_kv_heads;
   const int seq = sk / sh.num_kv_heads;
-  // Contexts are clamped to what the block table holds and to what the grid's
-  // splits cover, so no work-group reads past the table or the partials.
   const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
   int ctx = ctxl[seq];
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
-  const int head0 = kvh * sh.group + chunk * GT;
-  merge_partials<D, GT>(pacc, pml, out, (size_t)unit * sh.nsplit,
-                        ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
+  const int head0 = kvh * sh.group + chunk * sh.head_tile;
+  merge_partials<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, sh.head_tile,
+                           ((size_t)seq * sh.num_heads + head0) * D, ns_eff, msm);
 }
 
-template <int D, int GT, bool I8>
-hipError_t launch_decode_tile(const DecodeLaunch& l) {
+template <int D, int NW, bool I8>
+hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const DecodeShape& sh = l.shape;
   const int grid = ((sh.num_items + 7) / 8) * 8 * sh.nchunk;
   const auto* q = static_cast<const half_t*>(l.q);
@@ -426,35 +627,28 @@ hipError_t launch_decode_tile(const DecodeLaunch& l) {
   const auto* vc = static_cast<const uint8_t*>(l.v_cache);
   auto* out = static_cast<half_t*>(l.out);
   if (l.fused) {
-    decode_kernel<D, GT, I8, true><<<grid, kThreads, 0, l.stream>>>(
+    decode_kernel<D, NW, I8, true><<<grid, NW * kWave, 0, l.stream>>>(
         q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
         l.part_ml, l.counters, sh);
     return hipGetLastError();
   }
-  decode_kernel<D, GT, I8, false><<<grid, kThreads, 0, l.stream>>>(
+  decode_kernel<D, NW, I8, false><<<grid, NW * kWave, 0, l.stream>>>(
       q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc, l.part_ml,
       l.counters, sh);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
-  splitk_reduce_kernel<D, GT><<<units, kThreads, 0, l.stream>>>(l.part_acc, l.part_ml,
-                                                                l.context_lens, out, sh);
+  splitk_reduce_kernel<D><<<units, kThreads, 0, l.stream>>>(l.part_acc, l.part_ml, l.context_lens,
+                                                            out, sh);
   return hipGetLastError();
 }
 
 template <int D, bool I8>
 hipError_t launch_decode_dtype(const DecodeLaunch& l) {
-  switch (l.head_tile) {
-    case 1: return launch_decode_tile<D, 1, I8>(l);
-    case 2: return launch_decode_tile<D, 2, I8>(l);
-    case 3: return launch_decode_tile<D, 3, I8>(l);
-    case 4: return launch_decode_tile<D, 4, I8>(l);
-    case 5: return launch_decode_tile<D, 5, I8>(l);
-    case 6: return launch_decode_tile<D, 6, I8>(l);
-    case 7: return launch_decode_tile<D, 7, I8>(l);
-    case 8: return launch_decode_tile<D, 8, I8>(l);
-    default: return hipErrorInvalidValue;
+  if constexpr (D <= 128) {
+    if (l.waves == 8) return launch_decode_waves<D, 8, I8>(l);
   }
+  return launch_decode_waves<D, 4, I8>(l);
 }
 
 template <int D>

@@ -8,9 +8,8 @@
 
 namespace pa {
 
-constexpr int kWavesPerGroup = 4;    // waves per decode work-group
-constexpr int kIterTokens = 64;      // tokens one wave handles per iteration (4 slabs of 16)
-constexpr int kMaxGroupTile = 8;     // query heads sharing one KV read inside a work-group
+constexpr int kIterTokens = 64;      // partition granularity (one wave iteration for head_dim <= 128)
+constexpr int kMaxGroupTile = 16;    // query heads sharing one KV read (one MFMA column tile)
 
 // Shape of one decode launch, shared by every decode kernel.
 struct DecodeShape {
@@ -18,6 +17,7 @@ struct DecodeShape {
   int num_heads;
   int num_kv_heads;
   int group;        // num_heads / num_kv_heads
+  int head_tile;    // query heads per work-group (<= kMaxGroupTile)
   int nchunk;       // group / head_tile
   int block_size;
   int bs_log2;
@@ -42,7 +42,7 @@ struct DecodeLaunch {
   float* part_ml;      // [units, nsplit, head_tile, 2]
   uint32_t* counters;  // [units]
   int head_dim;
-  int head_tile;
+  int waves;           // waves per decode work-group: 4 or 8 (head_dim <= 128)
   bool int8_kv;
   bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
   DecodeShape shape;

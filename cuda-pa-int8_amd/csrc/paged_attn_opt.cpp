@@ -272,5 +272,7 @@ PYBIND11_MODULE(paged_attn_opt, m) {
   m.def("decode_plan", &decode_plan, "(partition_tokens, num_splits) the launcher would use");
   m.def("reshape_and_cache_int8", &reshape_and_cache_int8,
         "per-token INT8 quantize + paged cache write (new op)");
+  m.def("set_waves_per_group", [](int64_t w) { check_status(pa_decode_set_waves_per_group((int32_t)w)); },
+        "tuning hook: force 4 or 8 waves per decode work-group (0 = automatic)");
   m.def("version", []() { return std::string(pa_version()); });
 }

@@ -22,7 +22,9 @@
  * the kernels stay memory-safe when they are broken):
  *   - context_lens[s] <= 0 gives out[s] = 0 (the torch shim rejects it first,
  *     as the reference does);
- *   - context_lens[s] > max_blocks_per_seq * block_size is clamped to it;
+ *   - context_lens[s] is clamped to max_blocks_per_seq * block_size and, when
+ *     max_context_len > 0 is passed, to the split plan made for it (pass an
+ *     upper bound of every length, or <= 0);
  *   - a block id outside [0, num_blocks) contributes no tokens.
  *
  * Workspace: the decode entry points need device scratch of
@@ -95,6 +97,13 @@ size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_
                                  int32_t max_blocks_per_seq, int32_t max_context_len,
                                  int32_t partition_tokens);
 size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads);
+
+/* Tuning hook (no reference counterpart): force 4 or 8 waves per decode
+ * work-group for every later plan in this process; 0 restores the automatic
+ * choice (8 for head_dim <= 128, else 4).  Used by partition/occupancy
+ * sweeps; affects pa_decode_plan, pa_decode_workspace_bytes and the launches
+ * alike, so set it before sizing a workspace. */
+pa_status_t pa_decode_set_waves_per_group(int32_t waves);
 
 /* FP16 KV, single launch.  Replaces paged_decode_attn_warp
  * (kernels/paged_attention_v3_warp.cu:137-176; bound at kernels/bindings.cpp:50-51).

@@ -53,8 +53,6 @@ __all__ = [
     "dequantize_kv",
     "reshape_and_cache_int8",
     "gather_kv",
-    "decode_bytes",
-    "quant_write_bytes",
 ]
 
 
@@ -328,33 +326,3 @@ def reshape_and_cache_int8(key, value, slot_mapping, k_cache, v_cache,
     v_cache[phys, :, :, off] = vq[idx]
     k_scales[phys, :, off] = ks[idx]
     v_scales[phys, :, off] = vs[idx]
-
-
-# --------------------------------------------------------------------------
-# byte models used by bench.py (algorithmic bytes; padding not counted)
-# --------------------------------------------------------------------------
-
-def decode_bytes(context_lens, num_heads, num_kv_heads, head_dim,
-                 block_size=16, kv_elem_bytes=2, scales=False):
-    """Algorithmic HBM bytes of one decode call.
-
-    K+V of every live token once, plus the per-token fp32 scales for INT8,
-    plus q and out (fp16) and the block-table entries actually read, plus
-    the context lengths.
-    """
-    ctx = np.asarray(context_lens, dtype=np.int64)
-    s_ = len(ctx)
-    tok = int(ctx.sum())
-    b = tok * num_kv_heads * head_dim * 2 * kv_elem_bytes
-    if scales:
-        b += tok * num_kv_heads * 2 * 4
-    b += 2 * s_ * num_heads * head_dim * 2
-    b += 4 * int(((ctx + block_size - 1) // block_size).sum())
-    b += 4 * s_
-    return b
-
-
-def quant_write_bytes(num_tokens, num_kv_heads, head_dim):
-    """Algorithmic bytes of one quantize+write call over ``num_tokens``."""
-    t = num_tokens * num_kv_heads
-    return t * head_dim * 2 * 2 + t * head_dim * 2 + t * 2 * 4 + 8 * num_tokens

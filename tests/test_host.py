@@ -1,0 +1,172 @@
+"""CPU tests of the host side: the C-ABI library, its validation and planning
+logic, the torch shim's error paths and the byte model.  No GPU needed."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pa_mi355x.h")
+
+
+@pytest.fixture(scope="module")
+def lib(built):
+    import pa_int8
+
+    return pa_int8.capi()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(built):
+    lib_path, _ = built
+    so = ctypes.CDLL(lib_path)
+    names = declared_functions()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(so, n)]
+    assert not missing, missing
+
+
+def test_prototypes_cover_the_header(built):
+    from pa_int8 import _loader
+
+    assert set(declared_functions()) == set(_loader.PROTOTYPES)
+
+
+def test_version_and_status_strings(lib):
+    assert b"gfx950" in lib.pa_version()
+    for code in range(8):
+        assert lib.pa_status_string(code)
+    assert lib.pa_status_string(99) == b"unknown status"
+
+
+# validate: the reference's TORCH_CHECK rules (v3:149-150, v5:167-168, v5:176)
+@pytest.mark.parametrize("bs,f16_ok,i8_ok", [(8, True, False), (16, True, True), (32, True, True),
+                                             (64, True, True), (128, True, True), (24, False, False),
+                                             (256, False, False), (0, False, False), (4, False, False)])
+def test_validate_block_size_rule(lib, bs, f16_ok, i8_ok):
+    f16 = lib.pa_validate_decode(0, 2, 8, 128, 2, 10, bs, 8, 4)
+    i8 = lib.pa_validate_decode(2, 2, 8, 128, 2, 10, bs, 8, 4)
+    assert (f16 == 0) == f16_ok and (i8 == 0) == i8_ok
+    if not f16_ok:
+        assert f16 == 3
+
+
+def test_validate_shape_rules(lib):
+    assert lib.pa_validate_decode(0, 2, 8, 128, 2, 10, 16, 4, 4) == 4      # x != 8
+    assert lib.pa_validate_decode(0, 2, 8, 96, 2, 10, 16, 8, 4) == 4       # head_dim not built
+    assert lib.pa_validate_decode(0, 2, 8, 128, 3, 10, 16, 8, 4) == 2      # H % Hkv
+    assert lib.pa_validate_decode(0, 2, 8, 128, 2, 0, 16, 8, 4) == 2       # no blocks
+    assert lib.pa_validate_decode(0, 0, 8, 128, 2, 0, 16, 8, 0) == 0       # empty batch is fine
+    for d in (64, 128, 256):
+        assert lib.pa_validate_decode(3, 1, 32, d, 1, 1, 16, 8, 1) == 0
+
+
+def test_check_context_lens(lib):
+    mx = ctypes.c_int32(0)
+    a = (ctypes.c_int32 * 3)(5, 9, 2)
+    assert lib.pa_check_context_lens(ctypes.cast(a, ctypes.c_void_p), 3, ctypes.byref(mx)) == 0
+    assert mx.value == 9
+    b = (ctypes.c_int32 * 2)(8, 0)
+    assert lib.pa_check_context_lens(ctypes.cast(b, ctypes.c_void_p), 2, None) == 7
+
+
+@pytest.mark.parametrize("s,h,hkv,ctx", [(32, 12, 2, 4096), (64, 12, 2, 8192), (8, 32, 8, 131072),
+                                         (256, 32, 1, 32768), (4, 8, 8, 512), (1, 8, 1, 1)])
+def test_plan_invariants(lib, s, h, hkv, ctx):
+    part, ns = ctypes.c_int32(), ctypes.c_int32()
+    mb = (ctx + 15) // 16
+    for kind in range(4):
+        assert lib.pa_decode_plan(kind, s, h, 128, hkv, 16, mb, ctx, 0, ctypes.byref(part),
+                                  ctypes.byref(ns)) == 0
+        assert part.value % 64 == 0 and part.value >= 64
+        assert ns.value >= 1 and part.value * ns.value >= ctx
+        assert part.value * (ns.value - 1) < ctx
+        need = lib.pa_decode_workspace_bytes(kind, s, h, 128, hkv, 16, mb, ctx, 0)
+        assert need % 256 == 0 and need >= lib.pa_decode_counter_bytes(s, h, hkv)
+    # forced partition sizes are rounded up to 64 tokens
+    assert lib.pa_decode_plan(0, s, h, 128, hkv, 16, mb, ctx, 100, ctypes.byref(part),
+                              ctypes.byref(ns)) == 0
+    assert part.value == min(128, (ctx + 63) // 64 * 64)
+
+
+def test_waves_override_hook(lib):
+    assert lib.pa_decode_set_waves_per_group(3) == 2
+    for w in (4, 8, 0):
+        assert lib.pa_decode_set_waves_per_group(w) == 0
+
+
+def test_decode_rejects_missing_workspace(lib):
+    # host-side refusal before any device access: NULL workspace
+    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, ctypes.c_float(0.1), 16, 2, 8, 128, 2,
+                                       10, 8, 4, 0, 0, None, 0, None)
+    assert st == 5
+    st = lib.pa_paged_decode_attn_warp(None, 1, 1, 1, 1, 1, ctypes.c_float(0.1), 16, 2, 8, 128, 2,
+                                       10, 8, 4, 0, 0, None, 0, None)
+    assert st == 1
+
+
+def test_quant_write_host_checks(lib):
+    args = [16, 16, 1024, 512, 1024, 512, 16, 4, 2, 128, 16, 16, 16, 16, 10]
+    assert lib.pa_reshape_and_cache_int8(*args, 8, 8, None) == 3          # block_size 8
+    assert lib.pa_reshape_and_cache_int8(*args, 16, 4, None) == 4         # x = 4
+    bad = list(args)
+    bad[2] = 1001                                                         # unaligned stride
+    assert lib.pa_reshape_and_cache_int8(*bad, 16, 8, None) == 2
+
+
+def test_torch_shim_rejects_cpu_tensors(built):
+    import torch
+
+    import pa_int8
+
+    q = torch.zeros(2, 8, 128, dtype=torch.float16)
+    kc = torch.zeros(4, 2, 16, 16, 8, dtype=torch.float16)
+    vc = torch.zeros(4, 2, 128, 16, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32)
+    ln = torch.ones(2, dtype=torch.int32)
+    for name, fn in pa_int8.VARIANTS.items():
+        with pytest.raises(RuntimeError, match="CUDA"):
+            fn(torch.empty_like(q), q, kc, vc, bt, ln, 0.1, 16)
+    for name, fn in pa_int8.VARIANTS_INT8.items():
+        with pytest.raises(RuntimeError, match="CUDA"):
+            fn(torch.empty_like(q), q, kc.to(torch.int8), vc.to(torch.int8),
+               torch.ones(4, 2, 16), torch.ones(4, 2, 16), bt, ln, 0.1, 16)
+
+
+def test_registry_mirrors_reference_names(built):
+    import inspect
+
+    import cuda_ext
+    import pa_int8
+
+    assert set(cuda_ext.VARIANTS) == {"warp", "splitk"}
+    assert set(cuda_ext.VARIANTS_INT8) == {"warp_int8", "splitk_int8"}
+    p16 = list(inspect.signature(pa_int8.VARIANTS["warp"]).parameters)
+    assert p16 == ["out", "q", "k_cache", "v_cache", "block_table", "context_lens", "scale",
+                   "block_size"]
+    p8 = list(inspect.signature(pa_int8.VARIANTS_INT8["splitk_int8"]).parameters)
+    assert p8 == ["out", "q", "k_cache", "v_cache", "k_scales", "v_scales", "block_table",
+                  "context_lens", "scale", "block_size"]
+
+
+def test_byte_model_closed_forms():
+    from pa_int8 import metrics
+
+    assert metrics.decode_bytes([4096] * 32, 12, 2, 128) == 134_447_232
+    assert metrics.decode_bytes([8192] * 64, 12, 2, 128, kv_elem_bytes=1,
+                                scales=True) == 277_348_608
+    assert metrics.decode_bytes([8192] * 64, 12, 2, 128) == 537_395_456
+    assert metrics.decode_bytes([32768] * 8, 32, 8, 128) == 1_073_938_464
+    assert metrics.decode_bytes([131072] * 8, 32, 8, 128) == 4_295_360_544
+    assert metrics.decode_bytes([131072] * 8, 32, 8, 128, kv_elem_bytes=1,
+                                scales=True) == 2_214_985_760
+    assert metrics.quant_write_bytes(64 * 8192, 2, 128) == 817_889_280
+    assert metrics.decode_kv_bytes([4096] * 32, 2, 128) == 134_217_728

@@ -13,7 +13,6 @@ Each oracle function is checked against something other than itself:
 * build_paged_kv_cache(_int8), dequantize_kv, reshape_and_cache_int8 --
   gather round trips, the golden dequant vectors and cross-agreement of the
   two placement routes.
-* decode_bytes -- the closed-form byte counts of the benchmark configs.
 """
 
 import math
@@ -293,18 +292,3 @@ def test_reshape_and_cache_matches_builder_placement():
     ref.reshape_and_cache_int8(k[:1, 0], v[:1, 0], np.array([ekc.shape[0] * 16]), ekc, evc, eks,
                                evs)
     assert np.array_equal(before, ekc)
-
-
-# ------------------------------------------------------------------ byte model
-
-def test_decode_bytes_closed_forms():
-    # config 2: 32 x 4096, 12/2, D=128
-    assert ref.decode_bytes([4096] * 32, 12, 2, 128) == 134_447_232
-    # config 3 at 64 x 8192: INT8 and FP16
-    assert ref.decode_bytes([8192] * 64, 12, 2, 128, kv_elem_bytes=1, scales=True) == 277_348_608
-    assert ref.decode_bytes([8192] * 64, 12, 2, 128) == 537_395_456
-    # config 4, FP16 at 32k / 128k, INT8 at 128k
-    assert ref.decode_bytes([32768] * 8, 32, 8, 128) == 1_073_938_464
-    assert ref.decode_bytes([131072] * 8, 32, 8, 128) == 4_295_360_544
-    assert ref.decode_bytes([131072] * 8, 32, 8, 128, kv_elem_bytes=1, scales=True) == 2_214_985_760
-    assert ref.quant_write_bytes(64 * 8192, 2, 128) == 817_889_280
