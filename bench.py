@@ -36,7 +36,7 @@ for _p in (ROOT, PKG_ROOT):
 
 METRIC = "decode µs + achieved HBM GB/s (% of peak), FP16 vs INT8 KV, GQA 12/2 d128"
 MALL_BYTES = 256 << 20
-ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5"]
+ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "ceiling"]
 
 
 def log(*a):
@@ -179,7 +179,7 @@ def decode_steps(torch, case, variant, partition=0):
 # --------------------------------------------------------------------------- configs
 
 def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0, outliers=False,
-                   replays=3, eager=False, partition=0):
+                   replays=3, eager=False, partition=0, eager_only=False):
     from pa_int8 import metrics
 
     int8 = variant.endswith("int8")
@@ -187,7 +187,12 @@ def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0,
     case = make_case(torch, lens, h, hkv, d, 16, "cuda", seed, int8, outliers,
                      copies_for(per_copy))
     fns, _ = decode_steps(torch, case, variant, partition)
-    ms = time_steps(torch, fns, steps, warmup, replays)
+    if eager_only:
+        for i in range(warmup):
+            fns[i % len(fns)]()
+        ms = time_eager(torch, fns, steps)
+    else:
+        ms = time_steps(torch, fns, steps, warmup, replays)
     nbytes = metrics.decode_bytes(lens, h, hkv, d, kv_elem_bytes=1 if int8 else 2, scales=int8)
     import pa_int8
 
@@ -298,6 +303,46 @@ def run_configs(torch, names, steps, warmup):
     return out
 
 
+# --------------------------------------------------------------------------- ceiling probes
+
+def read_ceiling(torch, nbytes=134_217_728):
+    """Practical HBM read rate at the headline's size, from the library's
+    streaming-read probes: a contiguous sweep and 4 KB chunks in random order
+    (the paged-cache access pattern); best grid of a few, MALL-rotated."""
+    import pa_int8
+
+    lib = pa_int8.capi()
+    copies = copies_for(nbytes)
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    nchunk = nbytes // 4096
+    order = torch.randperm(nchunk, device="cuda").to(torch.int32)
+    res = {}
+    for name in ("contiguous", "chunks_4k_random"):
+        best = 0.0
+        for grid in (1024, 2048, 4096):
+            def mk(b):
+                def f():
+                    s = torch.cuda.current_stream().cuda_stream
+                    if name == "contiguous":
+                        st = lib.pa_probe_read_contiguous(b.data_ptr(), nbytes, sink.data_ptr(),
+                                                          grid, s)
+                    else:
+                        st = lib.pa_probe_read_chunks(b.data_ptr(), nbytes, order.data_ptr(),
+                                                      nchunk, 4096, sink.data_ptr(), grid, s)
+                    assert st == 0, st
+                return f
+            ms = time_steps(torch, [mk(b) for b in bufs], 40, 4, 3)
+            best = max(best, nbytes / (ms * 1e-3) / 1e9)
+        res[name + "_gbs"] = round(best, 1)
+    res["bytes"] = nbytes
+    res["copies_rotated"] = copies
+    del bufs
+    torch.cuda.empty_cache()
+    log(f"[bench] read ceiling at {nbytes} B: {res}")
+    return res
+
+
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(seconds):
@@ -351,6 +396,11 @@ def main():
                     help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time the headline with plain launches instead of a HIP graph "
+                         "(used under rocprofv3 counter collection)")
+    ap.add_argument("--pmc-copy", action="store_true",
+                    help="also run a 256 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -373,21 +423,32 @@ def main():
     # ---- headline: config 2, single-launch FP16
     lens = [4096] * 32
     head = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "warp", args.steps, args.warmup,
-                          replays=1, eager=True)
+                          replays=1, eager=True, eager_only=args.eager)
     head_sk = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "splitk", args.steps, args.warmup)
     ms = head["us"] / 1e3
     nbytes = head["algo_bytes"]
     achieved = nbytes / (ms * 1e-3) / 1e9
 
     configs = {"cfg2_qwen_fp16_warp": head, "cfg2_qwen_fp16_splitk": head_sk}
+    if args.pmc_copy:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     configs.update(run_configs(torch, [n for n in names if n != "cfg2"], args.steps,
                                args.warmup))
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic_cfg2_warp.md")
     if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("cfg2_warp_bytes_per_launch")
+        # line "traffic_bytes_per_launch: N" of the committed counter summary
+        for line in open(tpath):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1].strip())
+
+    ceiling = read_ceiling(torch) if "ceiling" in names or args.configs == "all" else None
 
     cpu = None
     if not args.no_cpu:
@@ -427,6 +488,7 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "read_ceiling": ceiling,
         "configs": configs,
     }
     print(json.dumps(line), flush=True)

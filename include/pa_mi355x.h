@@ -166,6 +166,19 @@ pa_status_t pa_reshape_and_cache_int8(
     void* k_cache, void* v_cache, float* k_scales, float* v_scales,
     int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
 
+/* Measurement helpers (no reference counterpart): streaming-read probes that
+ * give bench.py the practical HBM read rate next to the decode numbers.
+ * pa_probe_read_contiguous sweeps `bytes` from `src` with 16-byte loads;
+ * pa_probe_read_chunks reads `num_chunks` chunks of `chunk_bytes` (a multiple
+ * of 4096) at src + order[i] * chunk_bytes, skipping order values past
+ * `bytes`.  Both keep a checksum that is written to `sink` only on a
+ * practically impossible value, so the loads cannot be optimised away. */
+pa_status_t pa_probe_read_contiguous(const void* src, size_t bytes, uint32_t* sink, int32_t grid,
+                                     pa_stream_t stream);
+pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* order,
+                                 int32_t num_chunks, int32_t chunk_bytes, uint32_t* sink,
+                                 int32_t grid, pa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
