@@ -305,42 +305,47 @@ def run_configs(torch, names, steps, warmup):
 
 # --------------------------------------------------------------------------- ceiling probes
 
-def read_ceiling(torch, nbytes=134_217_728):
-    """Practical HBM read rate at the headline's size, from the library's
-    streaming-read probes: a contiguous sweep and 4 KB chunks in random order
-    (the paged-cache access pattern); best grid of a few, MALL-rotated."""
+def read_ceiling(torch, sizes=(134_217_728, 1_073_741_824)):
+    """Practical HBM read rates from the library's streaming-read probes: a
+    contiguous sweep and chunks in random order -- 4 KB (one FP16 K or V tile
+    of a block, D=128) and 2 KB (one INT8 tile) -- at the headline's size and
+    at 1 GiB; best grid of a few, MALL-rotated."""
     import pa_int8
 
     lib = pa_int8.capi()
-    copies = copies_for(nbytes)
-    bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
-    nchunk = nbytes // 4096
-    order = torch.randperm(nchunk, device="cuda").to(torch.int32)
-    res = {}
-    for name in ("contiguous", "chunks_4k_random"):
-        best = 0.0
-        for grid in (1024, 2048, 4096):
-            def mk(b):
-                def f():
-                    s = torch.cuda.current_stream().cuda_stream
-                    if name == "contiguous":
-                        st = lib.pa_probe_read_contiguous(b.data_ptr(), nbytes, sink.data_ptr(),
-                                                          grid, s)
-                    else:
-                        st = lib.pa_probe_read_chunks(b.data_ptr(), nbytes, order.data_ptr(),
-                                                      nchunk, 4096, sink.data_ptr(), grid, s)
-                    assert st == 0, st
-                return f
-            ms = time_steps(torch, [mk(b) for b in bufs], 40, 4, 3)
-            best = max(best, nbytes / (ms * 1e-3) / 1e9)
-        res[name + "_gbs"] = round(best, 1)
-    res["bytes"] = nbytes
-    res["copies_rotated"] = copies
-    del bufs
-    torch.cuda.empty_cache()
-    log(f"[bench] read ceiling at {nbytes} B: {res}")
-    return res
+    out = {}
+    for nbytes in sizes:
+        copies = copies_for(nbytes)
+        bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        res = {}
+        for name, chunk in (("contiguous", 0), ("chunks_4k_random", 4096),
+                            ("chunks_2k_random", 2048)):
+            nchunk = nbytes // chunk if chunk else 0
+            order = (torch.randperm(nchunk, device="cuda").to(torch.int32) if chunk else sink)
+            best = 0.0
+            for grid in (1024, 2048, 4096):
+                def mk(b, grid=grid, chunk=chunk, nchunk=nchunk, order=order):
+                    def f():
+                        s = torch.cuda.current_stream().cuda_stream
+                        if not chunk:
+                            st = lib.pa_probe_read_contiguous(b.data_ptr(), nbytes,
+                                                              sink.data_ptr(), grid, s)
+                        else:
+                            st = lib.pa_probe_read_chunks(b.data_ptr(), nbytes, order.data_ptr(),
+                                                          nchunk, chunk, sink.data_ptr(), grid, s)
+                        assert st == 0, st
+                    return f
+                steps = 40 if nbytes < (1 << 29) else 10
+                ms = time_steps(torch, [mk(b) for b in bufs], steps, 4, 3)
+                best = max(best, nbytes / (ms * 1e-3) / 1e9)
+            res[name + "_gbs"] = round(best, 1)
+        res["copies_rotated"] = copies
+        out[str(nbytes)] = res
+        del bufs
+        torch.cuda.empty_cache()
+        log(f"[bench] read ceiling at {nbytes} B: {res}")
+    return out
 
 
 # --------------------------------------------------------------------------- CPU baseline

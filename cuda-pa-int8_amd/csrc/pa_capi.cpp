@@ -21,7 +21,6 @@ constexpr int kRefTile = 128;        // reference TILE (paged_attention_v3_warp.
 // round trips, larger ones leave CUs idle.
 constexpr int kTargetWaves = 2048;   // waves one decode launch aims for (256 CUs x 8)
 constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
-constexpr int kMaxPartition = 4096;  // per 4 waves: caps the serial work of a work-group
 std::atomic<int> g_waves_override{0};
 constexpr size_t kAlign = 256;
 
@@ -65,13 +64,14 @@ Plan make_plan(int num_seqs, int num_heads, int num_kv_heads, int head_dim, int 
   long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
   if (ctx < 1) ctx = 1;
   long long part;
+  // Caps the serial work of a work-group and keeps a split's block ids in LDS.
+  const long long hi = (long long)pa::kMaxPartitionPer4Waves * p.waves / 4;
   if (partition_tokens > 0) {
-    part = partition_tokens;
+    part = std::min<long long>(partition_tokens, hi);
   } else {
     const long long units = std::max(1, p.units);
     const long long groups = kTargetWaves / p.waves;
     const long long lo = (long long)kMinPartition * p.waves / 4;
-    const long long hi = (long long)kMaxPartition * p.waves / 4;
     part = (ctx * units + groups - 1) / groups;
     part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
     part = std::min(std::max(part, lo), hi);

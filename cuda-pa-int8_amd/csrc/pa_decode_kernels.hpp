@@ -1,14 +1,14 @@
 // Paged-attention decode kernels for gfx950 (FP16 and INT8 KV), MFMA form.
 //
 // Work decomposition
-//   A work item is (sequence, kv_head, split).  A work-group of 4 waves serves
+//   A work item is (sequence, kv_head, split).  A work-group of 4 or 8 waves serves
 //   one work item for the whole group of query heads that share the kv head
 //   (up to 16), so every K/V byte fetched from HBM feeds all of them (the
 //   reference launches one block per query head and re-reads KV G times,
 //   kernels/paged_attention_v3_warp.cu:159).  The split's tokens are cut into
-//   wave iterations (64 tokens for head_dim <= 128, else 32) dealt round-robin
-//   to the 4 waves; each wave keeps its own online-softmax state and the waves
-//   merge through LDS at the end.
+//   wave iterations (64 tokens for head_dim <= 128, else 32) that the waves
+//   claim from an LDS counter as their loads return; each wave keeps its own
+//   online-softmax state and the waves merge through LDS at the end.
 //
 // Both products are 16-wide MFMAs (v_mfma_f32_16x16x32_f16):
 //   QK:  S^T[16 token rows][16 heads] += K[rows][32 dims] x Q^T[32 dims][heads]
@@ -51,6 +51,9 @@
 namespace pa {
 
 constexpr int kThreads = 4 * kWave;   // split-K reduce work-group
+// s_waitcnt immediate (gfx9 encoding) that waits for LDS/scalar memory only:
+// vmcnt and expcnt at their maxima, lgkmcnt = 0.
+constexpr int kWaitLgkm0 = 0xC07F;
 constexpr float kNegInf = -INFINITY;
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -118,12 +121,27 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
                                                half_t* __restrict__ out, size_t part_base, int gt,
                                                size_t out_base, int ns, MergeSmem& msm) {
   constexpr int PER = (16 * D + THREADS - 1) / THREADS;
-  constexpr int SB = 4;   // splits per batch of accumulator loads
+  constexpr int SB = PER >= 16 ? 1 : 16 / PER;   // splits per batch: 16 loads in flight per thread
   auto ld = [](const float* p) -> float {
     if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else return *p;
   };
   const int tid = threadIdx.x;
+  // Accumulator loads of one batch of SB splits (zeros past the end).
+  float v[SB][PER];
+  auto load_batch = [&](int sb, int se) {
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int idx = tid + i * THREADS;
+        const int hh = idx / D, d = idx - hh * D;
+        const int sp = sb + u;
+        v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((part_base + sp) * gt + hh) * D + d) : 0.f;
+      }
+  };
+  // The first batch goes out with the (m, l) loads: one round trip for both.
+  load_batch(0, min(ns, 64));
   // Per head h: 16 threads (one DPP row) own the splits k, k+16, k+32, ...
   const int h = tid >> 4, k = tid & 15;
   const bool hv = h < gt;
@@ -175,16 +193,7 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
     }
     __syncthreads();
     for (int sb = s0; sb < se; sb += SB) {
-      float v[SB][PER];
-#pragma unroll
-      for (int u = 0; u < SB; ++u)
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const int idx = tid + i * THREADS;
-          const int hh = idx / D, d = idx - hh * D;
-          const int sp = sb + u;
-          v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((part_base + sp) * gt + hh) * D + d) : 0.f;
-        }
+      if (sb != 0) load_batch(sb, se);
 #pragma unroll
       for (int u = 0; u < SB; ++u)
 #pragma unroll
@@ -204,11 +213,20 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
   }
 }
 
+// Block ids of one split: at most kMaxPartitionPer4Waves * NW / 4 tokens,
+// starting anywhere inside a block of >= kMinBlockSize tokens.
+template <int NW>
+constexpr int split_blocks_max() {
+  return kMaxPartitionPer4Waves * NW / 4 / kMinBlockSize + 1;
+}
+
 template <int D, int NW>
 struct alignas(16) DecodeSmem {
   float a[NW / 2][16][D];   // merge slots: per head, per dim
   float m[NW / 2][16];
   float l[NW / 2][16];
+  int blk[split_blocks_max<NW>()];   // the split's block ids
+  int next_it;                       // next unclaimed wave iteration
   int last;
   MergeSmem merge;
 };
@@ -296,11 +314,25 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   int e_cur = I8 ? 0 : 14;
   const float c = sh.scale_log2;
 
-  // ---- software-pipelined token loop.  In iteration `it` the block ids of
-  // the wave's next iteration are loaded first; its K rows are issued as soon
-  // as the QK MFMAs have consumed this iteration's K registers, and its V rows
-  // (plus INT8 scales) as soon as the PV MFMAs have consumed the V registers,
-  // so HBM traffic of the next iteration overlaps this iteration's math.
+  // ---- the split's block ids, staged once in LDS.
+  const int b_first = t_begin >> bsl;
+  const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1,
+                                         split_blocks_max<NW>())
+                                   : 0;
+  for (int i = threadIdx.x; i < nblk; i += NW * kWave) sm.blk[i] = btrow[b_first + i];
+  if (threadIdx.x == 0) sm.next_it = NW;
+  // LDS-only barrier: the writes above are complete (lgkmcnt 0) before it,
+  // and no vector-memory wait is implied.
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+
+  // ---- software-pipelined token loop over wave iterations claimed
+  // dynamically: each wave starts with iteration w and, once the K rows of
+  // its current iteration have arrived and fed the QK MFMAs, claims the next
+  // unclaimed one from an LDS counter and issues its K rows; its V rows (plus
+  // INT8 scales) follow once the PV MFMAs have consumed the V registers.  HBM
+  // traffic of the next iteration overlaps this iteration's math, and waves
+  // whose loads return early take over work from slower ones.
   struct Blocks {
     int kb[PAIRS];
     int vb[PAIRS];
@@ -315,9 +347,17 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
     for (int p = 0; p < PAIRS; ++p) {
       const int kg = tok0 + 32 * p + 8 * (r >> 2);
       const int tg = tok0 + 32 * p + 8 * g;
-      b.kb[p] = btrow[(kg < t_end ? kg : t_begin) >> bsl];
-      b.vb[p] = btrow[(tg < t_end ? tg : t_begin) >> bsl];
+      const int ki = ((kg < t_end ? kg : t_begin) >> bsl) - b_first;
+      const int vi = ((tg < t_end ? tg : t_begin) >> bsl) - b_first;
+      b.kb[p] = sm.blk[ki < nblk ? ki : 0];
+      b.vb[p] = sm.blk[vi < nblk ? vi : 0];
     }
+  };
+  auto claim = [&]() -> int {
+    int v = 0;
+    if (lane == 0)
+      v = __hip_atomic_fetch_add(&sm.next_it, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane(v);
   };
   // K rows: token tok0 + 32p + 8(r>>2) + (r&3) (first MFMA) and + 4 (second).
   auto issue_k = [&](int it_, const Blocks& b) {
@@ -367,138 +407,159 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
     }
   };
 
+  // The loop is rotated so that every load inside it is unconditional: the
+  // body issues the next K, finishes the current iteration (softmax, PV),
+  // issues the next V, then runs QK of the next iteration and claims the one
+  // after.  The wait for K inside the body therefore never covers the V rows
+  // issued after it; the last iteration's softmax and PV run after the loop.
   if (w < n_it) {
-    Blocks b0;
-    load_blocks(w, b0);
-    issue_k(w, b0);
-    issue_v(w, b0);
-  }
-  for (int it = w; it < n_it; it += NW) {
-    const bool has_next = it + NW < n_it;
-    Blocks bn;
-    if (has_next) load_blocks(it + NW, bn);
-    // Tokens past the end or in invalid blocks exist only in the last
-    // iteration of a split (or with a corrupt block table): mask only then.
-    const bool need_mask =
-        __builtin_amdgcn_ballot_w64(nvalid[0] < 8 || nvalid[PAIRS - 1] < 8) != 0;
-
-    // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r
-    float s[PAIRS][8];
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-      f4_t sx = {0.f, 0.f, 0.f, 0.f}, sy = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KC; ++kk) {
-        h8_t ax, ay;
-        if constexpr (I8) {
-          ax = i8x8_biased(kx[p][kk]);
-          ay = i8x8_biased(ky[p][kk]);
-        } else {
-          ax = __builtin_bit_cast(h8_t, kx[p][kk]);
-          ay = __builtin_bit_cast(h8_t, ky[p][kk]);
-        }
-        sx = mfma16(ax, qreg[kk], sx);
-        sy = mfma16(ay, qreg[kk], sy);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[p][e] = sx[e];
-        s[p][4 + e] = sy[e];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (has_next) issue_k(it + NW, bn);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- online softmax (lane-local except the per-head max)
-    float mloc = kNegInf;
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float v;
-        if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
-        else v = s[p][j] * c;
-        s[p][j] = v;
-      }
-    if (need_mask) {
+    auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask) {
+      // ---- online softmax (lane-local except the per-head max)
+      float mloc = kNegInf;
 #pragma unroll
       for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          s[p][j] = j < nvalid[p] ? s[p][j] : kNegInf;
-          if constexpr (I8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
+          float v;
+          if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
+          else v = s[p][j] * c;
+          s[p][j] = v;
         }
-    }
+      if (need_mask) {
 #pragma unroll
-    for (int p = 0; p < PAIRS; ++p)
+        for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) mloc = fmaxf(mloc, s[p][j]);
-    const float m_new = fmaxf(m_run, head_max(mloc));
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha_m = exp2f_fast(m_run - m_use);   // rescales l
-    float alpha_acc = alpha_m;                         // rescales acc (incl. weight exponent)
-    m_run = m_new;
-    float wsc;
-    if constexpr (I8) {
-      float msv = 0.f;
+          for (int j = 0; j < 8; ++j) {
+            s[p][j] = j < nvalid[p] ? s[p][j] : kNegInf;
+            if constexpr (I8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
+          }
+      }
 #pragma unroll
       for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
-      // Every head's lanes see the same tokens, so this max is wave-uniform.
-      msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
-      // Keep the weight exponent while the largest weight stays in [2^12, 2^15).
-      const float top = __builtin_amdgcn_ldexpf(msv, e_cur);
-      if (msv > 0.f && (top >= 32768.f || top < 4096.f)) {
-        int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
-        e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
-        alpha_acc = __builtin_amdgcn_ldexpf(alpha_m, e_new - e_cur);
-        e_cur = e_new;
-      }
-      wsc = __builtin_amdgcn_ldexpf(1.f, e_cur);
-    } else {
-      wsc = 16384.f;
-    }
-    float lsum = 0.f;
-    h8_t pb[PAIRS];
+        for (int j = 0; j < 8; ++j) mloc = fmaxf(mloc, s[p][j]);
+      const float m_new = fmaxf(m_run, head_max(mloc));
+      const float m_use = m_new == kNegInf ? 0.f : m_new;
+      const float alpha_m = exp2f_fast(m_run - m_use);   // rescales l
+      float alpha_acc = alpha_m;                         // rescales acc (incl. weight exponent)
+      m_run = m_new;
+      float wsc;
+      if constexpr (I8) {
+        float msv = 0.f;
 #pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
+        for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float pj = exp2f_fast(s[p][j] - m_use);
-        lsum += pj;
-        float wj;
-        if constexpr (I8) wj = pj * vsv[p][j] * wsc;
-        else wj = pj * wsc;
-        pb[p][j] = (half_t)wj;
-      }
-    }
-    l_part = l_part * alpha_m + lsum;
-    if (__builtin_amdgcn_ballot_w64(alpha_acc != 1.f) != 0) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] *= alpha_acc;
-    }
-
-    // ---- PV
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        h8_t av;
-        if constexpr (I8) {
-          av = i8x8_exact(vr[p][t]);
-        } else {
-          uint4 v = vr[p][t];
-          if (need_mask) v = keep_first(v, nvalid[p]);
-          av = __builtin_bit_cast(h8_t, v);
+          for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
+        // Every head's lanes see the same tokens, so this max is wave-uniform.
+        msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
+        // Keep the weight exponent while the largest weight stays in [2^12, 2^15).
+        const float top = __builtin_amdgcn_ldexpf(msv, e_cur);
+        if (msv > 0.f && (top >= 32768.f || top < 4096.f)) {
+          int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
+          e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
+          alpha_acc = __builtin_amdgcn_ldexpf(alpha_m, e_new - e_cur);
+          e_cur = e_new;
         }
-        acc[t] = mfma16(av, pb[p], acc[t]);
+        wsc = __builtin_amdgcn_ldexpf(1.f, e_cur);
+      } else {
+        wsc = 16384.f;
       }
+      float lsum = 0.f;
+      h8_t pb[PAIRS];
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pj = exp2f_fast(s[p][j] - m_use);
+          lsum += pj;
+          float wj;
+          if constexpr (I8) wj = pj * vsv[p][j] * wsc;
+          else wj = pj * wsc;
+          pb[p][j] = (half_t)wj;
+        }
+      }
+      l_part = l_part * alpha_m + lsum;
+      if (__builtin_amdgcn_ballot_w64(alpha_acc != 1.f) != 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] *= alpha_acc;
+      }
+
+      // ---- PV
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          h8_t av;
+          if constexpr (I8) {
+            av = i8x8_exact(vr[p][t]);
+          } else {
+            uint4 v = vr[p][t];
+            if (need_mask) v = keep_first(v, nvalid[p]);
+            av = __builtin_bit_cast(h8_t, v);
+          }
+          acc[t] = mfma16(av, pb[p], acc[t]);
+        }
+      }
+    };
+    auto qk = [&](float (&s)[PAIRS][8]) {
+      // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+        f4_t sx = {0.f, 0.f, 0.f, 0.f}, sy = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+          h8_t ax, ay;
+          if constexpr (I8) {
+            ax = i8x8_biased(kx[p][kk]);
+            ay = i8x8_biased(ky[p][kk]);
+          } else {
+            ax = __builtin_bit_cast(h8_t, kx[p][kk]);
+            ay = __builtin_bit_cast(h8_t, ky[p][kk]);
+          }
+          sx = mfma16(ax, qreg[kk], sx);
+          sy = mfma16(ay, qreg[kk], sy);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[p][e] = sx[e];
+          s[p][4 + e] = sy[e];
+        }
+      }
+    };
+    auto mask_needed = [&]() {
+      // Tokens past the end or in invalid blocks exist only in the last
+      // iteration of a split (or with a corrupt block table).
+      bool short_lane = false;
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) short_lane = short_lane || nvalid[p] < 8;
+      return __builtin_amdgcn_ballot_w64(short_lane) != 0;
+    };
+    {
+      Blocks b0;
+      load_blocks(w, b0);
+      issue_k(w, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_v(w, b0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    float s[PAIRS][8];
+    qk(s);
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next) issue_v(it + NW, bn);
-    __builtin_amdgcn_sched_barrier(0);
+    int nxt = claim();
+    while (nxt < n_it) {
+      Blocks bn;
+      load_blocks(nxt, bn);
+      issue_k(nxt, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      softmax_pv(s, mask_needed());
+      __builtin_amdgcn_sched_barrier(0);
+      issue_v(nxt, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      qk(s);
+      __builtin_amdgcn_sched_barrier(0);
+      nxt = claim();
+    }
+    softmax_pv(s, mask_needed());
   }
 
   // ---- per-wave results: m (head r), l, acc (dims 16t + 4g + e)

@@ -10,6 +10,10 @@ namespace pa {
 
 constexpr int kIterTokens = 64;      // partition granularity (one wave iteration for head_dim <= 128)
 constexpr int kMaxGroupTile = 16;    // query heads sharing one KV read (one MFMA column tile)
+// Largest split, per 4 waves of a work-group.  The planner never exceeds it
+// (forced partitions included), so the block ids of one split fit in LDS.
+constexpr int kMaxPartitionPer4Waves = 4096;
+constexpr int kMinBlockSize = 8;
 
 // Shape of one decode launch, shared by every decode kernel.
 struct DecodeShape {

@@ -2,6 +2,10 @@
 // plain contiguous sweep and for chunks in an arbitrary order (the access
 // pattern of a block-permuted paged cache).  Measurement helpers for
 // bench.py's roofline context; not part of the decode path.
+//
+// Both probes keep several independent 16-byte loads per lane in flight and
+// fold every loaded word into a checksum, so the compiler can neither narrow
+// nor drop a load.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -9,32 +13,64 @@
 
 namespace {
 
-__global__ void __launch_bounds__(256)
+constexpr int kProbeThreads = 256;
+constexpr int kUnroll = 4;   // independent 16-B loads per lane per step
+
+__device__ __forceinline__ uint32_t fold(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+
+__global__ void __launch_bounds__(kProbeThreads)
 probe_read_contiguous(const uint4* __restrict__ p, size_t n16, uint32_t* __restrict__ sink) {
   uint32_t acc = 0;
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
-    const uint4 v = p[i];
-    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  const size_t step = (size_t)gridDim.x * kProbeThreads * kUnroll;
+  size_t i = (size_t)blockIdx.x * kProbeThreads * kUnroll + threadIdx.x;
+  for (; i + (kUnroll - 1) * kProbeThreads < n16; i += step) {
+    uint4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = p[i + u * kProbeThreads];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);
   }
+  for (int u = 0; u < kUnroll; ++u)   // ragged end of the sweep
+    if (i + u * kProbeThreads < n16) acc ^= fold(p[i + u * kProbeThreads]);
   if (acc == 0x9E3779B9u) sink[0] = acc;   // keeps the loads live; practically never taken
 }
 
-// One wave reads one chunk (chunk_bytes, a multiple of 4 KB) per step.
-__global__ void __launch_bounds__(256)
+// Each wave reads 4 KB per step (4 loads per lane): one 4 KB piece of a chunk,
+// or, for chunks below 4 KB, several chunks at once.  chunk_bytes is a
+// multiple of 1 KB that divides 4 KB or is a multiple of 4 KB.
+__global__ void __launch_bounds__(kProbeThreads)
 probe_read_chunks(const uint4* __restrict__ p, const int32_t* __restrict__ order, int32_t nchunk,
                   int32_t total, int32_t c16, uint32_t* __restrict__ sink) {
   uint32_t acc = 0;
-  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int wave = (blockIdx.x * kProbeThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
-  const int nw = (gridDim.x * blockDim.x) >> 6;
-  for (int b = wave; b < nchunk; b += nw) {
-    const int32_t c = order[b];
-    if ((uint32_t)c >= (uint32_t)total) continue;
-    const uint4* q = p + (size_t)c * c16;
-    for (int j = lane; j < c16; j += 64) {
-      const uint4 v = q[j];
-      acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  const int nw = (gridDim.x * kProbeThreads) >> 6;
+  if (c16 >= 64 * kUnroll) {
+    for (int b = wave; b < nchunk; b += nw) {
+      const int32_t c = order[b];
+      if ((uint32_t)c >= (uint32_t)total) continue;
+      const uint4* q = p + (size_t)c * c16 + lane;
+      for (int j = 0; j < c16; j += 64 * kUnroll) {
+        uint4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = q[j + 64 * u];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);
+      }
+    }
+  } else {
+    const int per = 64 * kUnroll / c16;   // chunks per 4 KB step (2 or 4)
+    for (int b0 = wave * per; b0 < nchunk; b0 += nw * per) {
+      uint4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int e = 64 * u + lane;          // 16-B element of this step
+        const int b = b0 + e / c16;
+        const int32_t c = b < nchunk ? order[b] : -1;
+        v[u] = (uint32_t)c < (uint32_t)total ? p[(size_t)c * c16 + e % c16] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);
     }
   }
   if (acc == 0x9E3779B9u) sink[0] = acc;
@@ -48,7 +84,7 @@ pa_status_t pa_probe_read_contiguous(const void* src, size_t bytes, uint32_t* si
                                      pa_stream_t stream) {
   if (!src || !sink) return PA_ERR_NULL_POINTER;
   if (grid < 1 || reinterpret_cast<uintptr_t>(src) % 16 != 0) return PA_ERR_BAD_SHAPE;
-  probe_read_contiguous<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  probe_read_contiguous<<<grid, kProbeThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<const uint4*>(src), bytes / 16, sink);
   return hipGetLastError() == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
@@ -57,12 +93,13 @@ pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* o
                                  int32_t num_chunks, int32_t chunk_bytes, uint32_t* sink,
                                  int32_t grid, pa_stream_t stream) {
   if (!src || !order || !sink) return PA_ERR_NULL_POINTER;
-  if (grid < 1 || chunk_bytes < 4096 || chunk_bytes % 4096 != 0 || num_chunks < 0 ||
-      reinterpret_cast<uintptr_t>(src) % 16 != 0)
+  const bool small = chunk_bytes == 1024 || chunk_bytes == 2048;
+  if (grid < 1 || (!small && (chunk_bytes < 4096 || chunk_bytes % 4096 != 0)) ||
+      num_chunks < 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
     return PA_ERR_BAD_SHAPE;
   const size_t total = bytes / (size_t)chunk_bytes;
   if (total > (size_t)INT32_MAX) return PA_ERR_BAD_SHAPE;
-  probe_read_chunks<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  probe_read_chunks<<<grid, kProbeThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<const uint4*>(src), order, num_chunks, (int32_t)total, chunk_bytes / 16, sink);
   return hipGetLastError() == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }

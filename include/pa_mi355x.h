@@ -85,7 +85,9 @@ pa_status_t pa_check_context_lens(const int32_t* host_context_lens, int32_t num_
 /* Split plan: how many tokens each work-group covers (a multiple of 64)
  * and how many splits the longest sequence needs.  `max_context_len` <= 0
  * means "use max_blocks_per_seq * block_size".  `partition_tokens` > 0
- * forces the partition size (rounded up to a multiple of 64). */
+ * forces the partition size (rounded up to a multiple of 64 and capped at
+ * 1024 tokens per wave of the work-group: 8192 for head_dim <= 128, 4096
+ * for head_dim 256). */
 pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
                            int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
                            int32_t max_blocks_per_seq, int32_t max_context_len,
@@ -169,9 +171,9 @@ pa_status_t pa_reshape_and_cache_int8(
 /* Measurement helpers (no reference counterpart): streaming-read probes that
  * give bench.py the practical HBM read rate next to the decode numbers.
  * pa_probe_read_contiguous sweeps `bytes` from `src` with 16-byte loads;
- * pa_probe_read_chunks reads `num_chunks` chunks of `chunk_bytes` (a multiple
- * of 4096) at src + order[i] * chunk_bytes, skipping order values past
- * `bytes`.  Both keep a checksum that is written to `sink` only on a
+ * pa_probe_read_chunks reads `num_chunks` chunks of `chunk_bytes` (1024,
+ * 2048 or a multiple of 4096) at src + order[i] * chunk_bytes, skipping order
+ * values past `bytes`.  Both keep a checksum that is written to `sink` only on a
  * practically impossible value, so the loads cannot be optimised away. */
 pa_status_t pa_probe_read_contiguous(const void* src, size_t bytes, uint32_t* sink, int32_t grid,
                                      pa_stream_t stream);

@@ -97,6 +97,31 @@ def test_plan_invariants(lib, s, h, hkv, ctx):
     assert part.value == min(128, (ctx + 63) // 64 * 64)
 
 
+def test_forced_partition_is_capped(lib):
+    # a split holds at most 1024 tokens per wave of the work-group (its block
+    # ids are staged in LDS): 8192 at 8 waves (head_dim <= 128), 4096 at 4
+    part, ns = ctypes.c_int32(), ctypes.c_int32()
+    for d, cap in ((128, 8192), (64, 8192), (256, 4096)):
+        assert lib.pa_decode_plan(1, 8, 32, d, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
+                                  ctypes.byref(ns)) == 0
+        assert part.value == cap and ns.value == 131072 // cap
+    lib.pa_decode_set_waves_per_group(4)
+    try:
+        assert lib.pa_decode_plan(1, 8, 32, 128, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
+                                  ctypes.byref(ns)) == 0
+        assert part.value == 4096
+    finally:
+        lib.pa_decode_set_waves_per_group(0)
+
+
+def test_probe_host_checks(lib):
+    # rejected before any device access: chunk sizes outside {1, 2, 4k*n} KB
+    for chunk in (0, 512, 3072, 6144):
+        assert lib.pa_probe_read_chunks(16, 1 << 20, 16, 4, chunk, 16, 64, None) == 2
+    assert lib.pa_probe_read_chunks(None, 1 << 20, 16, 4, 4096, 16, 64, None) == 1
+    assert lib.pa_probe_read_contiguous(16, 1 << 20, 16, 0, None) == 2
+
+
 def test_waves_override_hook(lib):
     assert lib.pa_decode_set_waves_per_group(3) == 2
     for w in (4, 8, 0):
