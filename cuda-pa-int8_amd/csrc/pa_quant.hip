@@ -11,14 +11,22 @@
 //     v_cache[blk, h, :, off]    = q
 //     scales[blk, h, off]        = scale,   with slot = blk * block_size + off.
 //
-// One wave handles one job = (16 consecutive input tokens, kv head, K or V).
-// Lane l owns token l&15 and the dim groups (l>>4) + 4j (8 dims each, one
-// 16-B load).  amax is combined over the 4 lanes of a token with permlane
-// swaps.  K rows go out as 8-B stores per (token, dim group).  V is
-// transposed through LDS when the 16 tokens fill 16 consecutive, 16-aligned
-// slots (prefill), so each V row leaves as one 16-B store; otherwise it is
-// written byte by byte (decode append, scattered slots).
+// A job is (16 consecutive input tokens, kv head, K or V).  The grid holds as
+// many work-groups as the GPU keeps resident; each wave loops over jobs with a
+// grid stride and keeps the inputs of its next two jobs in flight while it
+// quantizes the current one.  Lane l owns token l&15 and the dim groups
+// (l>>4) + 4j (8 dims each, one 16-B load).  amax is combined over the 4
+// lanes of a token with permlane swaps.  Quantizing multiplies by the IEEE
+// reciprocal of the scale; an element whose product lies too close to a
+// rounding tie (or is not finite) is redone with the IEEE division, so every
+// byte equals the reference's.  K rows go out as 8-B stores per (token, dim
+// group).  V is transposed through LDS when the 16 tokens fill 16
+// consecutive, 16-aligned slots (prefill), so each V row leaves as one 16-B
+// store; otherwise it is written byte by byte (decode append, scattered
+// slots).
 #include <math.h>
+
+#include <algorithm>
 
 #include "pa_device.hpp"
 #include "pa_internal.hpp"
@@ -27,16 +35,71 @@ namespace pa {
 
 constexpr int kQuantWaves = 4;
 
-__device__ __forceinline__ uint32_t quant_pair_bytes(uint32_t h2bits, float s, int& b0, int& b1) {
-  const half2_t h = __builtin_bit_cast(half2_t, h2bits);
-  float r0 = __builtin_rintf((float)h.x / s);
-  float r1 = __builtin_rintf((float)h.y / s);
-  r0 = (r0 != r0) ? 0.f : fminf(fmaxf(r0, -127.f), 127.f);
-  r1 = (r1 != r1) ? 0.f : fminf(fmaxf(r1, -127.f), 127.f);
-  b0 = (int)r0;
-  b1 = (int)r1;
-  return ((uint32_t)(b0 & 0xFF)) | ((uint32_t)(b1 & 0xFF) << 8);
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+// |fl(x * fl(1/s)) - fl(x / s)| <= 127.5 * 2^-23 + 2^-18 < 1.9e-5 whenever
+// |x / s| < 128 (two roundings of the product, half an ulp of the quotient).
+// A product farther than this from every half-integer therefore rounds to the
+// same integer as the IEEE quotient the reference computes.
+constexpr float kTieGuard = 3.0e-5f;
+constexpr float kRoundMagic = 12582912.0f;   // 1.5 * 2^23: y + magic rounds y to an integer (RNE)
+
+// Exact path: rne(x / s) with IEEE division, clamped to [-127, 127], NaN -> 0.
+__device__ __forceinline__ uint32_t quant_exact_byte(float x, float s) {
+  float r = __builtin_rintf(x / s);
+  r = (r != r) ? 0.f : fminf(fmaxf(r, -127.f), 127.f);
+  return (uint32_t)((int)r) & 0xFFu;
 }
+
+// Quantizes the 8 fp16 values of one 16-B group to 8 bytes with the
+// reciprocal.  `slow` is set when some element's product lies within
+// kTieGuard of a half-integer (or is not finite): the fast byte is then not
+// provably the reference's and the caller redoes the group exactly.  With a
+// normal fp16 scale, |x / s| <= 127 * (1 + 2^-11) < 127.5 for every element of
+// the row, so no range check is needed here.
+__device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow) {
+  const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
+  uint32_t bytes[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
+    const float xs[2] = {(float)h.x, (float)h.y};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float y = xs[e] * r;
+      slow = slow || !(__builtin_fabsf(y - __builtin_rintf(y)) < 0.5f - kTieGuard);
+      bytes[2 * k + e] = __builtin_bit_cast(uint32_t, y + kRoundMagic);   // low byte = rne(y) mod 256
+    }
+  }
+  uint2 out;
+  out.x = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bytes[3], bytes[2], 0x0c0c0400u),
+                                __builtin_amdgcn_perm(bytes[1], bytes[0], 0x0c0c0400u), 0x05040100u);
+  out.y = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bytes[7], bytes[6], 0x0c0c0400u),
+                                __builtin_amdgcn_perm(bytes[5], bytes[4], 0x0c0c0400u), 0x05040100u);
+  return out;
+}
+
+// The exact path for one 16-B group.
+__device__ __forceinline__ uint2 quant_group_exact(uint4 xv, float s) {
+  const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
+  uint32_t b[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
+    b[2 * k] = quant_exact_byte((float)h.x, s);
+    b[2 * k + 1] = quant_exact_byte((float)h.y, s);
+  }
+  return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                    b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+}
+
+// The 16-B input groups of one job for one lane, and the lane's token slot.
+template <int D>
+struct QuantJob {
+  static constexpr int JQ = D / 32;   // 16-B groups per lane
+  uint4 x[JQ];
+  int64_t slot;
+};
 
 template <int D>
 __global__ void __launch_bounds__(kQuantWaves * kWave)
@@ -45,115 +108,173 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
                    int num_tokens, int num_kv_heads, int8_t* __restrict__ kc,
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
                    int num_blocks, int bs, int njobs) {
-  constexpr int JQ = D / 32;   // 16-B groups per lane
+  constexpr int JQ = QuantJob<D>::JQ;
   __shared__ __attribute__((aligned(16))) uint8_t tile[kQuantWaves][D * 16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int job = blockIdx.x * kQuantWaves + w;
-  if (job >= njobs) return;
-  const int is_v = job & 1;
-  const int th = job >> 1;
-  const int h = th % num_kv_heads;
-  const int t0 = (th / num_kv_heads) * 16;
   const int i = lane & 15, qq = lane >> 4;
-  const int tok = t0 + i;
-  const bool tv = tok < num_tokens;
   const int64_t pool = (int64_t)num_blocks * bs;
-  const int64_t slot = tv ? slots[tok] : -1;
-  const bool sok = slot >= 0 && slot < pool;
+  const int nw = gridDim.x * kQuantWaves;
+  int job = blockIdx.x * kQuantWaves + w;
+  if (job >= njobs) return;
 
-  const half_t* src = is_v ? value + (int64_t)(tv ? tok : 0) * vts + (int64_t)h * vhs
-                           : key + (int64_t)(tv ? tok : 0) * kts + (int64_t)h * khs;
-  uint4 x[JQ];
+  // Loads are unconditional (a token past the end reads the last token and is
+  // never stored), so the compiler's wait for one job never covers the loads
+  // of the jobs issued after it.
+  auto load = [&](int jb, QuantJob<D>& J) {
+    const int is_v = jb & 1;
+    const int th = jb >> 1;
+    const int h = th % num_kv_heads;
+    const int tok = (th / num_kv_heads) * 16 + i;
+    const int tc = tok < num_tokens ? tok : num_tokens - 1;
+    J.slot = slots[tc];
+    const half_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
+                             : key + (int64_t)tc * kts + (int64_t)h * khs;
 #pragma unroll
-  for (int j = 0; j < JQ; ++j) {
-    x[j] = tv ? *reinterpret_cast<const uint4*>(src + (qq + 4 * j) * 8) : make_uint4(0, 0, 0, 0);
-  }
+    for (int j = 0; j < JQ; ++j) J.x[j] = *reinterpret_cast<const uint4*>(src + (qq + 4 * j) * 8);
+  };
 
-  // amax over the token's D values as fp16 magnitude bits (ordered like the values;
-  // a NaN input gives NaN bits above +inf, so the scale becomes NaN as in torch).
-  uint32_t am = 0;
+  // Two jobs stay in flight ahead of the one being quantized.  A prefetch
+  // past the end reloads the current job, so every load in the loop is
+  // unconditional (those lines are cached).  The three job buffers keep their
+  // registers and rotate roles over a 3-way unrolled loop: copying a buffer
+  // whose loads are still in flight would make the compiler wait for them.
+  QuantJob<D> b0, b1, b2;
+  load(job, b0);
+  load(job + nw < njobs ? job + nw : job, b1);
+  auto step = [&](const QuantJob<D>& cur, QuantJob<D>& pf) {
+    const int nxt = job + nw;
+    const int nxt2 = job + 2 * nw;
+    load(nxt2 < njobs ? nxt2 : job, pf);   // past the end: reload this job (cached)
+    __builtin_amdgcn_sched_barrier(0);
+    const int is_v = job & 1;
+    const int th = job >> 1;
+    const int h = th % num_kv_heads;
+    const int t0 = (th / num_kv_heads) * 16;
+    const bool tv = t0 + i < num_tokens;
+    const int64_t slot = tv ? cur.slot : -1;
+    const bool sok = slot >= 0 && slot < pool;
+
+    // amax over the token's D values as fp16 magnitude bits (ordered like the
+    // values; a NaN input gives NaN bits above +inf, so the scale becomes NaN
+    // as in torch).
+    u16x2_t am2 = {0, 0};
 #pragma unroll
-  for (int j = 0; j < JQ; ++j) {
-    const uint32_t wv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+    for (int j = 0; j < JQ; ++j) {
+      const uint32_t wv[4] = {cur.x[j].x, cur.x[j].y, cur.x[j].z, cur.x[j].w};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = wv[k] & 0x7FFFu, hi = (wv[k] >> 16) & 0x7FFFu;
-      am = am > lo ? am : lo;
-      am = am > hi ? am : hi;
+      for (int k = 0; k < 4; ++k)
+        am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2_t, wv[k] & 0x7FFF7FFFu));
     }
-  }
-  am = rows_umax(am);
-  const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
-  const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
-  const float s = (float)(half_t)(a / 127.0f);        // fp16 division, RNE
+    uint32_t am = am2[0] > am2[1] ? am2[0] : am2[1];
+    am = rows_umax(am);
+    const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
+    const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
+    const float s = (float)(half_t)(a / 127.0f);        // fp16 division, RNE
+    const float r = 1.0f / s;                           // IEEE reciprocal (inf when s = 0)
+    // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
+    // sends the token's elements to the exact path.
+    const bool s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
 
-  // quantize: 8 bytes per dim group
-  uint2 qv[JQ];
-  int qb[JQ][8];
-#pragma unroll
-  for (int j = 0; j < JQ; ++j) {
-    const uint32_t wv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
-    uint32_t pk[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pk[k] = quant_pair_bytes(wv[k], s, qb[j][2 * k], qb[j][2 * k + 1]);
-    qv[j].x = pk[0] | (pk[1] << 16);
-    qv[j].y = pk[2] | (pk[3] << 16);
-  }
+    const int64_t blk = sok ? slot / bs : 0;
+    const int off = sok ? (int)(slot - blk * bs) : 0;
+    const int64_t bh = blk * num_kv_heads + h;   // (block, kv_head) row
 
-  const int64_t blk = sok ? slot / bs : 0;
-  const int off = sok ? (int)(slot - blk * bs) : 0;
-  const int64_t bh = blk * num_kv_heads + h;   // (block, kv_head) row
+    // V: 16 tokens filling one aligned 16-slot run of a block are transposed
+    // through LDS and leave as 16-B rows.
+    const int64_t slot0 = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot & 0xFFFFFFFF)) |
+                          ((int64_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32)) << 32);
+    const bool mine = tv && slot == slot0 + i;
+    const bool vfast = is_v && (t0 + 16 <= num_tokens) && slot0 >= 0 && (slot0 & 15) == 0 &&
+                       slot0 + 16 <= pool && __builtin_amdgcn_ballot_w64(!mine) == 0;
 
-  if (!is_v) {
-    if (sok) {
+    // One 16-B group at a time: quantize, fix rare elements exactly, store.
 #pragma unroll
-      for (int j = 0; j < JQ; ++j) {
-        const int o = qq + 4 * j;
-        *reinterpret_cast<uint2*>(kc + ((bh * (D / 8) + o) * bs + off) * 8) = qv[j];
+    for (int j = 0; j < JQ; ++j) {
+      bool slow = !s_normal;
+      uint2 qj = quant_group_fast(cur.x[j], r, slow);
+      if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+        if (slow) qj = quant_group_exact(cur.x[j], s);   // rare: the reference's division
       }
-      if (qq == 0) ksc[bh * bs + off] = s;
+      const int o = qq + 4 * j;   // dim group: dims 8o .. 8o+7
+      if (!is_v) {
+        if (sok) *reinterpret_cast<uint2*>(kc + ((bh * (D / 8) + o) * bs + off) * 8) = qj;
+      } else if (vfast) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          tile[w][(o * 8 + e) * 16 + i] = (uint8_t)((e < 4 ? qj.x : qj.y) >> (8 * (e & 3)));
+      } else if (sok) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          vc[(bh * D + o * 8 + e) * bs + off] = (int8_t)((e < 4 ? qj.x : qj.y) >> (8 * (e & 3)));
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    return;
-  }
+    if (vfast) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int64_t blk0 = slot0 / bs;
+      const int off0 = (int)(slot0 - blk0 * bs);
+      const int64_t bh0 = blk0 * num_kv_heads + h;
+#pragma unroll
+      for (int rr = lane; rr < D; rr += kWave) {
+        const uint4 row = *reinterpret_cast<const uint4*>(&tile[w][rr * 16]);
+        *reinterpret_cast<uint4*>(vc + (bh0 * D + rr) * bs + off0) = row;
+      }
+      // The tile is rewritten by this wave's next job only after every lane
+      // has read its rows.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (sok && qq == 0) (is_v ? vsc : ksc)[bh * bs + off] = s;
 
-  // V: 16 tokens filling one aligned 16-slot run of a block -> LDS transpose.
-  const int64_t slot0 = __builtin_amdgcn_readfirstlane((int)(slot & 0xFFFFFFFF)) |
-                        ((int64_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32)) << 32);
-  const bool mine = tv && slot == slot0 + i;
-  const bool fast = (t0 + 16 <= num_tokens) && slot0 >= 0 && (slot0 & 15) == 0 &&
-                    slot0 + 16 <= pool && __builtin_amdgcn_ballot_w64(!mine) == 0;
-  if (fast) {
-#pragma unroll
-    for (int j = 0; j < JQ; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tile[w][((qq + 4 * j) * 8 + e) * 16 + i] = (uint8_t)qb[j][e];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int64_t blk0 = slot0 / bs;
-    const int off0 = (int)(slot0 - blk0 * bs);
-    const int64_t bh0 = blk0 * num_kv_heads + h;
-#pragma unroll
-    for (int r = lane; r < D; r += kWave) {
-      const uint4 row = *reinterpret_cast<const uint4*>(&tile[w][r * 16]);
-      *reinterpret_cast<uint4*>(vc + (bh0 * D + r) * bs + off0) = row;
-    }
-  } else if (sok) {
-#pragma unroll
-    for (int j = 0; j < JQ; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vc[(bh * D + (qq + 4 * j) * 8 + e) * bs + off] = (int8_t)qb[j][e];
+    job = nxt;
+  };
+  // Whole rounds of three steps run without an exit test inside them: an exit
+  // in the middle of a round would give the compiler's wait-count analysis a
+  // path from a step with loads in flight to the loop head, and a full wait
+  // there.  The last 0-2 jobs follow the loop.
+  const int total = (njobs - job + nw - 1) / nw;   // jobs of this wave, >= 1
+  int k = 0;
+  for (; k + 3 <= total; k += 3) {
+    step(b0, b2);
+    step(b1, b0);
+    step(b2, b1);
   }
-  if (sok && qq == 0) vsc[bh * bs + off] = s;
+  if (k < total) step(b0, b2);
+  if (k + 1 < total) step(b1, b0);
+}
+
+// Work-groups the GPU holds at once for this kernel: the grid-stride loop is
+// sized to them so that no group starts after the others have finished.
+template <int D>
+int resident_groups() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256 * 4;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quant_write_kernel<D>,
+                                                     kQuantWaves * kWave, 0) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 4;
+    cache[dev] = cus * per_cu;
+  }
+  return cache[dev];
 }
 
 template <int D>
 static hipError_t launch_quant_d(const QuantLaunch& l) {
   const int tiles = (l.num_tokens + 15) / 16;
   const int njobs = tiles * l.num_kv_heads * 2;
-  const int grid = (njobs + kQuantWaves - 1) / kQuantWaves;
+  const int want = (njobs + kQuantWaves - 1) / kQuantWaves;
+  const int grid = std::min(want, resident_groups<D>());
   quant_write_kernel<D><<<grid, kQuantWaves * kWave, 0, l.stream>>>(
       static_cast<const half_t*>(l.key), static_cast<const half_t*>(l.value), l.key_token_stride,
       l.key_head_stride, l.value_token_stride, l.value_head_stride, l.slot_mapping, l.num_tokens,

@@ -42,6 +42,28 @@ def special_rows(d, rng):
     return np.stack(rows)
 
 
+_FP16 = np.arange(1 << 16, dtype=np.uint16).view(np.float16)
+_FP16 = _FP16[np.isfinite(_FP16)].astype(np.float32)
+
+
+def near_tie_rows(d, n, rng):
+    """Rows whose quotients x / scale lie within 2e-4 of a half-integer: the
+    inputs where x * (1/scale) and the IEEE quotient can round differently."""
+    rows = []
+    while len(rows) < n:
+        amax = np.float32(np.float16(rng.uniform(0.05, 3000.0)))
+        s = np.float32(np.float16(max(amax, np.float32(1e-8)) / np.float32(127)))
+        x = _FP16[np.abs(_FP16) <= amax]
+        qf = x / s
+        near = x[np.abs(np.abs(qf - np.floor(qf)) - np.float32(0.5)) < 2e-4]
+        if near.size < 4:
+            continue
+        row = rng.choice(near, size=d)
+        row[0] = amax                     # pins the scale
+        rows.append(row)
+    return np.stack(rows).astype(np.float16)
+
+
 def make_kv(T, hkv, d, rng):
     k = rng.standard_normal((T, hkv, d)).astype(np.float32)
     v = rng.standard_normal((T, hkv, d)).astype(np.float32) * 3.0
@@ -82,9 +104,9 @@ def slots_for(pattern, T, num_blocks, bs, rng):
     raise ValueError(pattern)
 
 
-def run_case(T, hkv, d, bs, pattern, seed):
+def run_case(T, hkv, d, bs, pattern, seed, kv=None):
     rng = np.random.default_rng(seed)
-    k, v = make_kv(T, hkv, d, rng)
+    k, v = make_kv(T, hkv, d, rng) if kv is None else kv(T, hkv, d, rng)
     num_blocks = (T + bs - 1) // bs * 2 + 3
     slots = slots_for(pattern, T, num_blocks, bs, rng)
     kc = rng.integers(-128, 128, size=(num_blocks, hkv, d // 8, bs, 8)).astype(np.int8)
@@ -114,6 +136,18 @@ def run_case(T, hkv, d, bs, pattern, seed):
 @pytest.mark.parametrize("pattern", ["prefill", "scattered", "padding"])
 def test_quant_write_bitexact(head_dim, block_size, pattern):
     run_case(T=301, hkv=2, d=head_dim, bs=block_size, pattern=pattern, seed=head_dim + block_size)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("pattern", ["prefill", "scattered"])
+def test_quant_write_near_ties(head_dim, pattern):
+    """Every element near a rounding tie: the kernel's reciprocal fast path must
+    hand these to the exact division (bit-exact with the IEEE quotient)."""
+    def kv(T, hkv, d, rng):
+        k = near_tie_rows(d, T * hkv, rng).reshape(T, hkv, d)
+        v = near_tie_rows(d, T * hkv, rng).reshape(T, hkv, d)
+        return k, v
+    run_case(T=96, hkv=2, d=head_dim, bs=16, pattern=pattern, seed=head_dim + 5, kv=kv)
 
 
 def test_quant_write_single_token_append():
