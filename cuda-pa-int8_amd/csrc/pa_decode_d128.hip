@@ -3,4 +3,5 @@
 
 namespace pa {
 hipError_t launch_decode_d128(const DecodeLaunch& l) { return launch_decode_d<128>(l); }
+int sched_groups_d128(int waves, bool int8_kv) { return sched_groups_d<128>(waves, int8_kv); }
 }  // namespace pa

@@ -3,4 +3,5 @@
 
 namespace pa {
 hipError_t launch_decode_d64(const DecodeLaunch& l) { return launch_decode_d<64>(l); }
+int sched_groups_d64(int waves, bool int8_kv) { return sched_groups_d<64>(waves, int8_kv); }
 }  // namespace pa

@@ -6,9 +6,10 @@
 //   (up to 16), so every K/V byte fetched from HBM feeds all of them (the
 //   reference launches one block per query head and re-reads KV G times,
 //   kernels/paged_attention_v3_warp.cu:159).  The split's tokens are cut into
-//   wave iterations (64 tokens for head_dim <= 128, else 32) that the waves
-//   claim from an LDS counter as their loads return; each wave keeps its own
-//   online-softmax state and the waves merge through LDS at the end.
+//   wave iterations (64 tokens for head_dim <= 128, else 32) dealt
+//   round-robin to the waves (a fixed assignment, so results are bitwise
+//   reproducible); each wave keeps its own online-softmax state and the waves
+//   merge through LDS at the end.
 //
 // Both products are 16-wide MFMAs (v_mfma_f32_16x16x32_f16):
 //   QK:  S^T[16 token rows][16 heads] += K[rows][32 dims] x Q^T[32 dims][heads]
@@ -111,22 +112,24 @@ struct MergeSmem {
 };
 
 // Merge the `ns` partials of one unit (gt heads) and write its fp16 output
-// rows.  Partials: acc[gt][D] (relative to m), then (m, l) per split and head.
+// rows.  The partial of split sp sits in slot slot0 + sp * stride: acc[gt][D]
+// (relative to m), and (m, l) per head.
 // COHERENT: read with device-coherent loads (partials written in this launch).
 // Loads are issued in independent batches so the merge costs a few memory
 // round trips, not one per split.  Called by every thread of the work-group.
 template <int D, int THREADS, bool COHERENT>
 __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
                                                const float* __restrict__ pml,
-                                               half_t* __restrict__ out, size_t part_base, int gt,
-                                               size_t out_base, int ns, MergeSmem& msm) {
+                                               half_t* __restrict__ out, size_t slot0, int stride,
+                                               int gt, size_t out_base, int ns, MergeSmem& msm) {
   constexpr int PER = (16 * D + THREADS - 1) / THREADS;
   constexpr int SB = PER >= 16 ? 1 : 16 / PER;   // splits per batch: 16 loads in flight per thread
   auto ld = [](const float* p) -> float {
     if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else return *p;
   };
-  const int tid = threadIdx.x;
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));   // nothing lane-dependent is hoisted out of a caller's loop
   // Accumulator loads of one batch of SB splits (zeros past the end).
   float v[SB][PER];
   auto load_batch = [&](int sb, int se) {
@@ -137,7 +140,7 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
         const int idx = tid + i * THREADS;
         const int hh = idx / D, d = idx - hh * D;
         const int sp = sb + u;
-        v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((part_base + sp) * gt + hh) * D + d) : 0.f;
+        v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((slot0 + (size_t)sp * stride) * gt + hh) * D + d) : 0.f;
       }
   };
   // The first batch goes out with the (m, l) loads: one round trip for both.
@@ -150,12 +153,12 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
   for (int u = 0; u < 4; ++u) {
     const int sp = k + 16 * u;
     const bool ok = hv && sp < ns;
-    const size_t pi = (part_base + sp) * gt + h;
+    const size_t pi = (slot0 + (size_t)sp * stride) * gt + h;
     mv[u] = ok ? ld(pml + pi * 2) : kNegInf;
     lv[u] = ok ? ld(pml + pi * 2 + 1) : 0.f;
   }
   float mx = kNegInf;
-  for (int sp = k + 64; hv && sp < ns; sp += 16) mx = fmaxf(mx, ld(pml + ((part_base + sp) * gt + h) * 2));
+  for (int sp = k + 64; hv && sp < ns; sp += 16) mx = fmaxf(mx, ld(pml + ((slot0 + (size_t)sp * stride) * gt + h) * 2));
 #pragma unroll
   for (int u = 0; u < 4; ++u) mx = fmaxf(mx, mv[u]);
   mx = fmaxf(mx, dpp_mov<kQuadXor1>(mx));
@@ -166,7 +169,7 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
 #pragma unroll
   for (int u = 0; u < 4; ++u) l += mv[u] == kNegInf ? 0.f : lv[u] * exp2f_fast(mv[u] - mx);
   for (int sp = k + 64; hv && sp < ns; sp += 16) {
-    const size_t pi = (part_base + sp) * gt + h;
+    const size_t pi = (slot0 + (size_t)sp * stride) * gt + h;
     const float m_s = ld(pml + pi * 2);
     if (m_s != kNegInf) l += ld(pml + pi * 2 + 1) * exp2f_fast(m_s - mx);
   }
@@ -187,7 +190,7 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
         if (hv && k + 16 * u < ns) msm.w[k + 16 * u][h] = mv[u] == kNegInf ? 0.f : exp2f_fast(mv[u] - mx);
     } else if (hv) {
       for (int sp = s0 + k; sp < se; sp += 16) {
-        const float m_s = ld(pml + ((part_base + sp) * gt + h) * 2);
+        const float m_s = ld(pml + ((slot0 + (size_t)sp * stride) * gt + h) * 2);
         msm.w[sp - s0][h] = m_s == kNegInf ? 0.f : exp2f_fast(m_s - mx);
       }
     }
@@ -226,18 +229,33 @@ struct alignas(16) DecodeSmem {
   float m[NW / 2][16];
   float l[NW / 2][16];
   int blk[split_blocks_max<NW>()];   // the split's block ids
-  int next_it;                       // next unclaimed wave iteration
   int last;
   MergeSmem merge;
 };
 
-template <int D, int NW, bool I8, bool FUSED>
-__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
-decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
-              const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
-              const float* __restrict__ vsc, const int* __restrict__ bt,
-              const int* __restrict__ ctxl, half_t* __restrict__ out, float* __restrict__ pacc,
-              float* __restrict__ pml, uint32_t* __restrict__ cnt, DecodeShape sh) {
+// One split of one unit, processed by a whole work-group.
+struct SplitWork {
+  int seq, kvh, chunk, split;
+  int ctx;         // context length (clamped)
+  int partition;   // tokens per split
+  int ns;          // splits of this unit
+  size_t slot0;    // partial slot of split 0 of this unit
+  int stride;      // partial slots between consecutive splits
+};
+
+// The decode of one split.  FUSED: partials are written device-coherent and
+// the last work-group of the unit merges them (single launch).  DIRECT1: a
+// unit with one split writes its output here (else the split-K reduce does).
+// `after_issue` runs in every wave once the wave's first K/V loads are issued
+// (the scheduled kernel claims its next item there, so that no wait for this
+// split's data also waits for the claim).
+template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, typename AfterIssue>
+__device__ __forceinline__ void decode_split(
+    const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
+    const float* __restrict__ ksc, const float* __restrict__ vsc, const int* __restrict__ bt,
+    half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
+    uint32_t* __restrict__ cnt, const DecodeShape& sh, const SplitWork& wk,
+    DecodeSmem<D, NW>& sm, AfterIssue&& after_issue) {
   constexpr int KC = D / 32;                 // 32-dim k-chunks of one QK product
   constexpr int NT = D / 16;                 // 16-dim output tiles of PV
   constexpr int PAIRS = D <= 128 ? 2 : 1;    // 32-token pairs per wave iteration
@@ -245,36 +263,20 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   constexpr int ESZ = I8 ? 1 : 2;            // bytes per cache element
   using LVec = typename std::conditional<I8, uint2, uint4>::type;   // 8 elements
 
-  static_assert(sizeof(DecodeSmem<D, NW>) <= 64 * 1024, "LDS budget");
-  __shared__ DecodeSmem<D, NW> sm;
-
-  // ---- work item (XCD-aware: the head chunks of one item share blockIdx % 8)
-  const int wg = blockIdx.x;
-  const int per_grp = 8 * sh.nchunk;
-  const int grp = wg / per_grp;
-  const int rem = wg - grp * per_grp;
-  const int chunk = rem >> 3;
-  const int item = grp * 8 + (rem & 7);
-  if (item >= sh.num_items) return;
-  const int split = item % sh.nsplit;
-  const int sk = item / sh.nsplit;
-  const int kvh = sk % sh.num_kv_heads;
-  const int seq = sk / sh.num_kv_heads;
+  const int seq = wk.seq, kvh = wk.kvh, chunk = wk.chunk, split = wk.split;
   const int gt = sh.head_tile;
-
-  // Contexts are clamped to what the block table holds and to what the grid's
-  // splits cover, so no work-group reads past the table or the partials.
-  const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
-  int ctx = ctxl[seq];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
-  if (split >= ns_eff) return;
-  const int t_begin = split * sh.partition;
-  const int t_end = min(ctx, t_begin + sh.partition);
+  const int ns_eff = wk.ns;
+  const int t_begin = split * wk.partition;
+  const int t_end = min(wk.ctx, t_begin + wk.partition);
   const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  // The thread index is made opaque here so that no lane-dependent address
+  // math is hoisted out of a caller's loop over splits (it would stay live,
+  // in registers, across the whole split).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
   const int head0 = kvh * sh.group + chunk * gt;
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
@@ -319,20 +321,17 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
   const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1,
                                          split_blocks_max<NW>())
                                    : 0;
-  for (int i = threadIdx.x; i < nblk; i += NW * kWave) sm.blk[i] = btrow[b_first + i];
-  if (threadIdx.x == 0) sm.next_it = NW;
+  for (int i = tid; i < nblk; i += NW * kWave) sm.blk[i] = btrow[b_first + i];
   // LDS-only barrier: the writes above are complete (lgkmcnt 0) before it,
   // and no vector-memory wait is implied.
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_s_barrier();
 
-  // ---- software-pipelined token loop over wave iterations claimed
-  // dynamically: each wave starts with iteration w and, once the K rows of
-  // its current iteration have arrived and fed the QK MFMAs, claims the next
-  // unclaimed one from an LDS counter and issues its K rows; its V rows (plus
-  // INT8 scales) follow once the PV MFMAs have consumed the V registers.  HBM
-  // traffic of the next iteration overlaps this iteration's math, and waves
-  // whose loads return early take over work from slower ones.
+  // ---- software-pipelined token loop: wave w takes iterations w, w + NW, ...
+  // Once the K rows of its current iteration have fed the QK MFMAs it issues
+  // the K rows of its next iteration; the V rows (plus INT8 scales) follow
+  // once the PV MFMAs have consumed the V registers.  HBM traffic of the next
+  // iteration overlaps this iteration's math.
   struct Blocks {
     int kb[PAIRS];
     int vb[PAIRS];
@@ -352,12 +351,6 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
       b.kb[p] = sm.blk[ki < nblk ? ki : 0];
       b.vb[p] = sm.blk[vi < nblk ? vi : 0];
     }
-  };
-  auto claim = [&]() -> int {
-    int v = 0;
-    if (lane == 0)
-      v = __hip_atomic_fetch_add(&sm.next_it, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    return __builtin_amdgcn_readfirstlane(v);
   };
   // K rows: token tok0 + 32p + 8(r>>2) + (r&3) (first MFMA) and + 4 (second).
   auto issue_k = [&](int it_, const Blocks& b) {
@@ -409,8 +402,7 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
 
   // The loop is rotated so that every load inside it is unconditional: the
   // body issues the next K, finishes the current iteration (softmax, PV),
-  // issues the next V, then runs QK of the next iteration and claims the one
-  // after.  The wait for K inside the body therefore never covers the V rows
+  // issues the next V, then runs QK of the next iteration.  The wait for K inside the body therefore never covers the V rows
   // issued after it; the last iteration's softmax and PV run after the loop.
   if (w < n_it) {
     auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask) {
@@ -542,10 +534,11 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
       issue_v(w, b0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    after_issue();
     float s[PAIRS][8];
     qk(s);
     __builtin_amdgcn_sched_barrier(0);
-    int nxt = claim();
+    int nxt = w + NW;
     while (nxt < n_it) {
       Blocks bn;
       load_blocks(nxt, bn);
@@ -557,9 +550,11 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
       __builtin_amdgcn_sched_barrier(0);
       qk(s);
       __builtin_amdgcn_sched_barrier(0);
-      nxt = claim();
+      nxt += NW;
     }
     softmax_pv(s, mask_needed());
+  } else {
+    after_issue();
   }
 
   // ---- per-wave results: m (head r), l, acc (dims 16t + 4g + e)
@@ -598,8 +593,7 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
 
   // ---- wave 0 holds the work-group result
   const size_t out_base = ((size_t)seq * sh.num_heads + head0) * D;
-  const size_t part_base = (size_t)unit * sh.nsplit;
-  const bool final_here = FUSED && ns_eff == 1;
+  const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
   if (w == 0 && r < gt) {
     if (final_here) {
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -610,7 +604,7 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
         *reinterpret_cast<uint2*>(out + out_base + (size_t)r * D + 16 * t + 4 * g) = pk;
       }
     } else {
-      const size_t pi = (part_base + split) * gt + r;
+      const size_t pi = (wk.slot0 + (size_t)split * wk.stride) * gt + r;
       float* pa = pacc + pi * D + 4 * g;
       if constexpr (FUSED) {
         // Device-coherent (write-through) stores: visible to every XCD once
@@ -650,13 +644,347 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
       }
       __syncthreads();
       if (sm.last) {
-        merge_partials<D, NW * kWave, true>(pacc, pml, out, part_base, gt, out_base, ns_eff,
-                                            sm.merge);
+        merge_partials<D, NW * kWave, true>(pacc, pml, out, wk.slot0, wk.stride, gt, out_base,
+                                            ns_eff, sm.merge);
         if (threadIdx.x == 0)
           __hip_atomic_store(cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
+}
+
+// Grid form: one work-group per (unit, split) slot of the host's plan.
+template <int D, int NW, bool I8, bool FUSED>
+__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
+              const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
+              const float* __restrict__ vsc, const int* __restrict__ bt,
+              const int* __restrict__ ctxl, half_t* __restrict__ out, float* __restrict__ pacc,
+              float* __restrict__ pml, uint32_t* __restrict__ cnt, DecodeShape sh) {
+  static_assert(sizeof(DecodeSmem<D, NW>) <= 64 * 1024, "LDS budget");
+  __shared__ DecodeSmem<D, NW> sm;
+
+  // ---- work item (XCD-aware: the head chunks of one item share blockIdx % 8)
+  const int wg = blockIdx.x;
+  const int per_grp = 8 * sh.nchunk;
+  const int grp = wg / per_grp;
+  const int rem = wg - grp * per_grp;
+  const int chunk = rem >> 3;
+  const int item = grp * 8 + (rem & 7);
+  if (item >= sh.num_items) return;
+  const int split = item % sh.nsplit;
+  const int sk = item / sh.nsplit;
+  const int kvh = sk % sh.num_kv_heads;
+  const int seq = sk / sh.num_kv_heads;
+
+  // Contexts are clamped to what the block table holds and to what the grid's
+  // splits cover, so no work-group reads past the table or the partials.
+  const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
+  int ctx = ctxl[seq];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
+  if (split >= ns_eff) return;
+  const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
+  const SplitWork wk{seq, kvh, chunk, split, ctx, sh.partition, ns_eff,
+                     (size_t)unit * sh.nsplit, 1};
+  decode_split<D, NW, I8, FUSED, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk, sm,
+                                        [] {});
+}
+
+// ---------------------------------------------------------------------------
+// In-kernel schedule: persistent work-groups over a compact work list.
+//
+// Every work-group reads the (clamped) context lengths and derives the same
+// schedule in LDS.  The partition P is chosen from the total token count:
+// about one item per resident work-group when all lengths are equal (the
+// grid plan's shape), about kSchedItemsPerGroup items per work-group
+// otherwise.  A row is one split of one sequence; rows that hold a full
+// partition come first, the shorter last rows of each sequence after them
+// (largest items first).  An item is (row, kv head, head chunk).  Items are
+// dealt to 8 claim classes by row, row % 8, with the kv heads and chunks of a
+// row next to each other; work-group b serves class b % 8 (its XCD under the
+// usual round-robin dispatch), starts with item b / 8 of its class
+// and claims the next one from the class counter once the current item's
+// first loads are issued.  Exactly as many claims as the class has items are
+// made per launch, so the claim that returns the last index is the last one
+// and resets the counter for the next launch.  No work-group is launched for
+// a split that a sequence does not have, whatever the block-table capacity or
+// the spread of the lengths.
+struct SchedArgs {
+  int* info;          // [1 + num_seqs]: partition, slot row base per sequence (for the reduce)
+  uint32_t* queue;    // 8 claim counters, kSchedQueueStride words apart
+  int rows_max;       // slot rows the partial buffers hold
+  int pmin, pmax;     // partition bounds (multiples of kIterTokens)
+};
+
+struct SchedSmem {
+  int full_pre[kSchedMaxSeqs + 1];   // exclusive prefix of full rows per sequence
+  int part_pre[kSchedMaxSeqs + 1];   // exclusive prefix of short last rows
+  int ctx[kSchedMaxSeqs];
+  uint32_t red[3][16];               // per-wave sum (in 1024-token units), min, max
+  int scan_f[16], scan_p[16];
+  int next_item;
+};
+
+// Unsigned wave reductions (DPP inside rows, permlane swaps across them);
+// every lane receives the result.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce_u(uint32_t v, Op op) {
+  v = op(v, dpp_mov_u<kQuadXor1>(v));
+  v = op(v, dpp_mov_u<kQuadXor2>(v));
+  v = op(v, dpp_mov_u<kRowHalfMirror>(v));
+  v = op(v, dpp_mov_u<kRowMirror>(v));
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = op(r[0], r[1]);
+  auto t = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return op(t[0], t[1]);
+}
+struct OpAddU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
+struct OpMinU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct OpMaxU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+
+// Inclusive prefix sum over the wave.
+__device__ __forceinline__ int wave_scan_i(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// Largest s in [0, n) with pre[s] <= x (pre is non-decreasing, pre[0] = 0 <= x).
+__device__ __forceinline__ int prefix_search(const int* pre, int n, int x) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= x) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+struct Schedule {
+  int partition, n_full, n_rows;
+  bool uniform;
+};
+
+// Builds the schedule in LDS; every thread of the work-group takes part and
+// returns the same values.  Thread t owns sequences [t*E, t*E + E).
+template <int NTH>
+__device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeShape& sh,
+                                   const SchedArgs& sa, SchedSmem& ss) {
+  constexpr int E = (kSchedMaxSeqs + NTH - 1) / NTH;
+  constexpr int NWV = NTH / kWave;
+  const int S = sh.num_seqs;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & (kWave - 1);
+  const int cap = sh.max_blocks * sh.block_size;
+  int c[E];
+  uint32_t tk = 0, mn = 0xFFFFFFFFu, mx = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid * E + e;
+    int v = i < S ? ctxl[i] : 0;
+    v = v < 0 ? 0 : (v > cap ? cap : v);
+    c[e] = v;
+    if (i < S) {
+      tk += (uint32_t)v >> 10;   // the total only steers the partition choice
+      mn = mn < (uint32_t)v ? mn : (uint32_t)v;
+      mx = mx > (uint32_t)v ? mx : (uint32_t)v;
+      ss.ctx[i] = v;
+    }
+  }
+  tk = wave_reduce_u(tk, OpAddU());
+  mn = wave_reduce_u(mn, OpMinU());
+  mx = wave_reduce_u(mx, OpMaxU());
+  if (lane == 0) {
+    ss.red[0][w] = tk;
+    ss.red[1][w] = mn;
+    ss.red[2][w] = mx;
+  }
+  __syncthreads();
+  uint64_t t = 0;
+  uint32_t a = 0xFFFFFFFFu, b = 0;
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) {
+    t += ss.red[0][i];
+    a = a < ss.red[1][i] ? a : ss.red[1][i];
+    b = b > ss.red[2][i] ? b : ss.red[2][i];
+  }
+  Schedule sc;
+  sc.uniform = a == b;
+  {
+    // P: about one item per resident work-group for equal lengths, about
+    // kSchedItemsPerGroup per work-group otherwise; within [pmin, pmax] and
+    // no longer than the longest sequence.
+    const uint64_t groups = gridDim.x;
+    const uint64_t k = sc.uniform ? 1 : kSchedItemsPerGroup;
+    uint64_t part = ((t << 10) * (uint64_t)sh.num_kv_heads + groups * k - 1) / (groups * k);
+    part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
+    part = part < (uint64_t)sa.pmin ? (uint64_t)sa.pmin : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
+    const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
+    sc.partition = (int)(part < top ? part : top);
+  }
+  // Exclusive scans of full rows (ctx / P) and short last rows (0 or 1); the
+  // partition doubles (rarely) until the rows fit the partial buffers, which
+  // hold them at the upper partition bound.
+  while (true) {
+    const int P = sc.partition;
+    int fs = 0, ps = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = tid * E + e;
+      fs += i < S ? c[e] / P : 0;
+      ps += i < S ? ((c[e] % P != 0 || c[e] == 0) ? 1 : 0) : 0;
+    }
+    const int fi = wave_scan_i(fs), pi = wave_scan_i(ps);
+    if (lane == kWave - 1) {
+      ss.scan_f[w] = fi;
+      ss.scan_p[w] = pi;
+    }
+    __syncthreads();
+    int fo = fi - fs, po = pi - ps, tf = 0, tp = 0;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) {
+      const int f = ss.scan_f[i], q = ss.scan_p[i];
+      if (i < w) {
+        fo += f;
+        po += q;
+      }
+      tf += f;
+      tp += q;
+    }
+    if (tf + tp > sa.rows_max && P < sa.pmax) {
+      __syncthreads();   // scan_f/scan_p are rewritten by the next pass
+      sc.partition = P * 2 < sa.pmax ? P * 2 : sa.pmax;
+      continue;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = tid * E + e;
+      if (i < S) {
+        ss.full_pre[i] = fo;
+        ss.part_pre[i] = po;
+        fo += c[e] / P;
+        po += (c[e] % P != 0 || c[e] == 0) ? 1 : 0;
+      }
+    }
+    if (tid == 0) {
+      ss.full_pre[S] = tf;
+      ss.part_pre[S] = tp;
+    }
+    sc.n_full = tf;
+    sc.n_rows = tf + tp;
+    break;
+  }
+  __syncthreads();
+  return sc;
+}
+
+template <int D, int NW, bool I8, bool FUSED>
+__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+decode_sched_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
+                    const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
+                    const float* __restrict__ vsc, const int* __restrict__ bt,
+                    const int* __restrict__ ctxl, half_t* __restrict__ out,
+                    float* __restrict__ pacc, float* __restrict__ pml, uint32_t* __restrict__ cnt,
+                    DecodeShape sh, SchedArgs sa) {
+  static_assert(sizeof(DecodeSmem<D, NW>) + sizeof(SchedSmem) <= 64 * 1024, "LDS budget");
+  __shared__ DecodeSmem<D, NW> sm;
+  __shared__ SchedSmem ss;
+  const Schedule sc = build_schedule<NW * kWave>(ctxl, sh, sa, ss);
+
+  const int S = sh.num_seqs, hkv = sh.num_kv_heads, nchunk = sh.nchunk;
+  const int P = __builtin_amdgcn_readfirstlane(sc.partition);
+  const int n_full = __builtin_amdgcn_readfirstlane(sc.n_full);
+  // Claim class of this work-group (its XCD under the usual round-robin
+  // dispatch): rows r with r % 8 == cls, each followed by its kv heads and
+  // head chunks, so every XCD reads every kv head and the chunks of one
+  // (row, kv head) run at about the same time on one XCD and share its L2.
+  const int n_rows = __builtin_amdgcn_readfirstlane(sc.n_rows);
+  const int per_row = hkv * nchunk;
+  const int cls = blockIdx.x & 7;
+  const int groups_c = ((int)gridDim.x - cls + 7) >> 3;
+  const int items_c = (n_rows > cls ? (n_rows - cls + 7) >> 3 : 0) * per_row;
+  uint32_t* queue = sa.queue + cls * kSchedQueueStride;
+  // Item indices are compared unsigned: whatever a claim counter holds, no
+  // work-group leaves its class's item list.
+  int idx = blockIdx.x >> 3;   // index within the class: static first item
+  while ((uint32_t)idx < (uint32_t)items_c) {
+    // The next item is claimed once this item's first loads are out.
+    uint32_t old = 0;
+    auto claim = [&] {
+      if (threadIdx.x == 0)
+        old = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    const int row = cls + 8 * (idx / per_row);
+    const int sub = idx - (idx / per_row) * per_row;
+    const int kvh = sub / nchunk, chunk = sub - (sub / nchunk) * nchunk;
+    // Item fields are work-group uniform: keep them in scalar registers.
+    int seq, split;
+    if (row < n_full) {
+      seq = prefix_search(ss.full_pre, S, row);
+      split = row - ss.full_pre[seq];
+    } else {
+      seq = prefix_search(ss.part_pre, S, row - n_full);
+      split = ss.full_pre[seq + 1] - ss.full_pre[seq];
+    }
+    seq = __builtin_amdgcn_readfirstlane(seq);
+    split = __builtin_amdgcn_readfirstlane(split);
+    const int ns = __builtin_amdgcn_readfirstlane(
+        (ss.full_pre[seq + 1] - ss.full_pre[seq]) + (ss.part_pre[seq + 1] - ss.part_pre[seq]));
+    const int rowbase = __builtin_amdgcn_readfirstlane(ss.full_pre[seq] + ss.part_pre[seq]);
+    const int ctx = __builtin_amdgcn_readfirstlane(ss.ctx[seq]);
+    const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
+                       ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
+    decode_split<D, NW, I8, FUSED, true>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
+                                         sm, claim);
+    // Every processed item of the class made one claim (the first item of
+    // each work-group is static), so the claim that returns items_c - 1 is
+    // the last one and resets the counter for the next launch.
+    if (threadIdx.x == 0) {
+      if (old == (uint32_t)(items_c - 1))
+        __hip_atomic_store(queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ss.next_item = (int)((uint32_t)groups_c + old);
+    }
+    __syncthreads();
+    idx = __builtin_amdgcn_readfirstlane(ss.next_item);
+  }
+  // The split-K reduce reads the partition and the slot row bases.
+  if (!FUSED && blockIdx.x == 0) {
+    if (threadIdx.x == 0) sa.info[0] = P;
+    for (int i = threadIdx.x; i < S; i += NW * kWave) sa.info[1 + i] = ss.full_pre[i] + ss.part_pre[i];
+  }
+}
+
+// Split-K reduce over the in-kernel schedule: one work-group per unit; units
+// with a single split were written by the partition kernel.
+template <int D>
+__global__ void __launch_bounds__(kThreads)
+sched_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
+                    const int* __restrict__ ctxl, const int* __restrict__ info,
+                    half_t* __restrict__ out, DecodeShape sh, int rows_max) {
+  __shared__ MergeSmem msm;
+  const int unit = blockIdx.x;
+  const int chunk = unit % sh.nchunk;
+  const int sk = unit / sh.nchunk;
+  const int kvh = sk % sh.num_kv_heads;
+  const int seq = sk / sh.num_kv_heads;
+  const int cap = sh.max_blocks * sh.block_size;
+  int ctx = ctxl[seq];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int P = info[0];
+  if (P < kIterTokens) return;   // (the partition kernel always writes it)
+  const int ns = ctx > 0 ? (ctx + P - 1) / P : 1;
+  if (ns <= 1) return;
+  const int rb = info[1 + seq];
+  if (rb < 0 || rb > rows_max - ns) return;   // slots stay inside the partial buffers
+  const size_t rowbase = (size_t)rb;
+  const int head0 = kvh * sh.group + chunk * sh.head_tile;
+  merge_partials<D, kThreads, false>(
+      pacc, pml, out, (rowbase * sh.num_kv_heads + kvh) * sh.nchunk + chunk,
+      sh.num_kv_heads * sh.nchunk, sh.head_tile, ((size_t)seq * sh.num_heads + head0) * D, ns, msm);
 }
 
 // Split-K reduce: one work-group per (seq, kv_head, head chunk).
@@ -675,13 +1003,35 @@ splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ p
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
   const int head0 = kvh * sh.group + chunk * sh.head_tile;
-  merge_partials<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, sh.head_tile,
-                           ((size_t)seq * sh.num_heads + head0) * D, ns_eff, msm);
+  merge_partials<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, 1, sh.head_tile,
+                                     ((size_t)seq * sh.num_heads + head0) * D, ns_eff, msm);
 }
 
 template <int D, int NW, bool I8>
 hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const DecodeShape& sh = l.shape;
+  if (l.sched) {
+    const SchedArgs sa{l.sched_info, l.queue, l.rows_max, l.pmin, l.pmax};
+    const auto* q = static_cast<const half_t*>(l.q);
+    const auto* kc = static_cast<const uint8_t*>(l.k_cache);
+    const auto* vc = static_cast<const uint8_t*>(l.v_cache);
+    auto* out = static_cast<half_t*>(l.out);
+    if (l.fused) {
+      decode_sched_kernel<D, NW, I8, true><<<l.groups, NW * kWave, 0, l.stream>>>(
+          q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
+          l.part_ml, l.counters, sh, sa);
+      return hipGetLastError();
+    }
+    decode_sched_kernel<D, NW, I8, false><<<l.groups, NW * kWave, 0, l.stream>>>(
+        q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
+        l.part_ml, l.counters, sh, sa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
+    sched_reduce_kernel<D><<<units, kThreads, 0, l.stream>>>(
+        l.part_acc, l.part_ml, l.context_lens, l.sched_info, out, sh, l.rows_max);
+    return hipGetLastError();
+  }
   const int grid = ((sh.num_items + 7) / 8) * 8 * sh.nchunk;
   const auto* q = static_cast<const half_t*>(l.q);
   const auto* kc = static_cast<const uint8_t*>(l.k_cache);
@@ -715,6 +1065,41 @@ hipError_t launch_decode_dtype(const DecodeLaunch& l) {
 template <int D>
 hipError_t launch_decode_d(const DecodeLaunch& l) {
   return l.int8_kv ? launch_decode_dtype<D, true>(l) : launch_decode_dtype<D, false>(l);
+}
+
+// Resident work-groups of the scheduled kernel for one head_dim (cached per
+// device and variant).
+template <int D>
+int sched_groups_d(int waves, bool int8_kv) {
+  static int cache[64][4] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int nw = (D <= 128 && waves == 8) ? 8 : 4;
+  const int slot = (nw == 8 ? 2 : 0) + (int8_kv ? 1 : 0);
+  if (cache[dev][slot] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    hipError_t e;
+    if (nw == 8) {
+      if constexpr (D <= 128) {
+        e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                          &per_cu, decode_sched_kernel<D, 8, true, true>, 8 * kWave, 0)
+                    : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                          &per_cu, decode_sched_kernel<D, 8, false, true>, 8 * kWave, 0);
+      } else {
+        e = hipErrorInvalidValue;
+      }
+    } else {
+      e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &per_cu, decode_sched_kernel<D, 4, true, true>, 4 * kWave, 0)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                        &per_cu, decode_sched_kernel<D, 4, false, true>, 4 * kWave, 0);
+    }
+    if (e != hipSuccess || per_cu <= 0 || cus <= 0) return 0;
+    cache[dev][slot] = cus * per_cu;
+  }
+  return cache[dev][slot];
 }
 
 }  // namespace pa

@@ -14,6 +14,12 @@ constexpr int kMaxGroupTile = 16;    // query heads sharing one KV read (one MFM
 // (forced partitions included), so the block ids of one split fit in LDS.
 constexpr int kMaxPartitionPer4Waves = 4096;
 constexpr int kMinBlockSize = 8;
+// In-kernel scheduling (persistent work-groups over a compact work list):
+// the lengths of up to kSchedMaxSeqs sequences are staged in LDS; a ragged
+// batch is cut into about kSchedItemsPerGroup items per resident work-group.
+constexpr int kSchedMaxSeqs = 1024;
+constexpr int kSchedItemsPerGroup = 4;
+constexpr int kSchedQueueStride = 32;   // words between the 8 claim counters (128 B)
 
 // Shape of one decode launch, shared by every decode kernel.
 struct DecodeShape {
@@ -50,8 +56,22 @@ struct DecodeLaunch {
   bool int8_kv;
   bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
   DecodeShape shape;
+  // In-kernel schedule (sched = true): `groups` resident work-groups claim
+  // (row, kv head) items; the partials hold `rows_max` slot rows.
+  bool sched;
+  int groups;
+  int rows_max;
+  int pmin, pmax;      // partition bounds, multiples of 64 (equal when forced)
+  int* sched_info;     // [1 + num_seqs]: partition, then the slot row base of each sequence
+  uint32_t* queue;     // 8 claim counters, zero between launches
   hipStream_t stream;
 };
+
+// Resident work-groups of the scheduled decode kernel (0 if it cannot run).
+// Defined in pa_decode_d{64,128,256}.hip.
+int sched_groups_d64(int waves, bool int8_kv);
+int sched_groups_d128(int waves, bool int8_kv);
+int sched_groups_d256(int waves, bool int8_kv);
 
 // Defined in pa_decode_d{64,128,256}.hip.
 hipError_t launch_decode_d64(const DecodeLaunch& l);

@@ -17,22 +17,38 @@ namespace {
 
 constexpr int64_t kRefTile = 128;
 
-// One zero-initialised workspace per (device, stream), grown on demand.  The
-// decode kernels leave its arrival counters at zero, so it is never cleared
-// again; calls on one stream are ordered by the stream itself.
+// One zero-initialised workspace per (device, stream), grown on demand; calls
+// on one stream are ordered by the stream itself.  A call needs its counter
+// region -- the first pa_decode_counter_bytes(...) bytes for its shape -- to be
+// zero, and leaves exactly that region zero; the bytes after it hold split
+// partials.  `zero_prefix` is the length known to be zero, so when a later
+// shape needs a longer counter region, the bytes between are cleared first
+// (with a fill kernel, which a HIP graph may also capture).
+struct Workspace {
+  at::Tensor buf;
+  size_t zero_prefix = 0;
+};
 std::mutex g_ws_mu;
-std::map<std::pair<int, void*>, at::Tensor> g_ws;
+std::map<std::pair<int, void*>, Workspace> g_ws;
 
-at::Tensor workspace_for(const at::Tensor& like, hipStream_t stream, size_t bytes) {
+at::Tensor workspace_for(const at::Tensor& like, hipStream_t stream, size_t bytes,
+                         size_t counter_bytes) {
   std::lock_guard<std::mutex> lk(g_ws_mu);
   const auto key = std::make_pair((int)like.get_device(), (void*)stream);
   auto it = g_ws.find(key);
-  if (it != g_ws.end() && (size_t)it->second.numel() >= bytes) return it->second;
-  size_t want = std::max<size_t>(bytes, 1 << 20);
-  if (it != g_ws.end()) want = std::max<size_t>(want, 2 * (size_t)it->second.numel());
-  at::Tensor t = at::zeros({(int64_t)want}, like.options().dtype(at::kByte));
-  g_ws[key] = t;
-  return t;
+  if (it == g_ws.end() || (size_t)it->second.buf.numel() < bytes) {
+    size_t want = std::max<size_t>(bytes, 1 << 20);
+    if (it != g_ws.end()) want = std::max<size_t>(want, 2 * (size_t)it->second.buf.numel());
+    Workspace w;
+    w.buf = at::zeros({(int64_t)want}, like.options().dtype(at::kByte));
+    w.zero_prefix = want;
+    it = g_ws.insert_or_assign(key, w).first;
+  }
+  Workspace& w = it->second;
+  if (counter_bytes > w.zero_prefix)
+    w.buf.narrow(0, (int64_t)w.zero_prefix, (int64_t)(counter_bytes - w.zero_prefix)).zero_();
+  w.zero_prefix = counter_bytes;   // the partials after it are written by this call
+  return w.buf;
 }
 
 void check_status(pa_status_t st) { TORCH_CHECK(st == PA_OK, pa_status_string(st)); }
@@ -116,7 +132,7 @@ void run_decode(pa_decode_kind_t kind, at::Tensor& out, const at::Tensor& q,
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
   const size_t need = pa_decode_workspace_bytes(kind, S, H, D, Hkv, (int32_t)block_size, MB,
                                                 max_ctx, (int32_t)partition_tokens);
-  at::Tensor ws = workspace_for(q, stream, need);
+  at::Tensor ws = workspace_for(q, stream, need, pa_decode_counter_bytes(S, H, Hkv));
   const float sc = (float)scale;
   pa_status_t st;
   auto ps = reinterpret_cast<pa_stream_t>(stream);

@@ -29,10 +29,14 @@
  *
  * Workspace: the decode entry points need device scratch of
  * pa_decode_workspace_bytes(...) bytes, 256-byte aligned.  Its first
- * pa_decode_counter_bytes(...) bytes are per-unit arrival counters that must
- * be zero before the first call; every call leaves them zero again, so a
- * workspace is zeroed once at allocation and then reused.  Two calls that
- * may run at the same time (different streams) need different workspaces.
+ * pa_decode_counter_bytes(...) bytes for the call's shape are arrival and
+ * claim counters that must be zero when the call starts; the call leaves
+ * exactly those bytes zero and uses the rest as scratch for split partials.
+ * A workspace zeroed at allocation can therefore be reused for calls of one
+ * shape without clearing; before a call whose counter region is longer than
+ * the previous call's, clear the bytes in between (they held partials).  Two
+ * calls that may run at the same time (different streams) need different
+ * workspaces.
  */
 #ifndef PA_MI355X_H
 #define PA_MI355X_H
@@ -82,8 +86,10 @@ pa_status_t pa_validate_decode(pa_decode_kind_t kind, int32_t num_seqs, int32_t 
 pa_status_t pa_check_context_lens(const int32_t* host_context_lens, int32_t num_seqs,
                                   int32_t* max_len);
 
-/* Split plan: how many tokens each work-group covers (a multiple of 64)
- * and how many splits the longest sequence needs.  `max_context_len` <= 0
+/* Split plan of the grid form: how many tokens each work-group covers (a
+ * multiple of 64) and how many splits the longest sequence needs.  (Under the
+ * in-kernel schedule the kernel picks the partition on the device from the
+ * actual lengths; a forced partition_tokens is used as given by both.)  `max_context_len` <= 0
  * means "use max_blocks_per_seq * block_size".  `partition_tokens` > 0
  * forces the partition size (rounded up to a multiple of 64 and capped at
  * 1024 tokens per wave of the work-group: 8192 for head_dim <= 128, 4096
@@ -106,6 +112,17 @@ size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_
  * sweeps; affects pa_decode_plan, pa_decode_workspace_bytes and the launches
  * alike, so set it before sizing a workspace. */
 pa_status_t pa_decode_set_waves_per_group(int32_t waves);
+
+/* Tuning hook (no reference counterpart): how later decode calls in this
+ * process distribute work.  0 = automatic: the in-kernel schedule for the
+ * split-K kinds with up to 1024 sequences, the grid otherwise; 1 = grid: one
+ * work-group per (unit, split) slot of the host plan; 2 = in-kernel schedule:
+ * persistent work-groups, one per resident slot, claim (split, kv head, head
+ * chunk) items of a compact work list that every work-group derives from
+ * context_lens, so no work-group is launched for a split a sequence does not
+ * have and the partition follows the actual lengths.  Set it before sizing a
+ * workspace. */
+pa_status_t pa_decode_set_schedule(int32_t mode);
 
 /* FP16 KV, single launch.  Replaces paged_decode_attn_warp
  * (kernels/paged_attention_v3_warp.cu:137-176; bound at kernels/bindings.cpp:50-51).

@@ -1,0 +1,158 @@
+"""GPU tests of the two work distributions of the decode kernels.
+
+``pa_decode_set_schedule`` selects the grid form (one work-group per
+(unit, split) slot of the host plan) or the in-kernel schedule (persistent
+work-groups over a compact work list built from context_lens on the device).
+Both must give the oracle's result on ragged batches, capacity-sized block
+tables, many sequences and zero-length sequences; the schedule's claim
+counters must return to zero after every launch (checked by running
+different shapes back to back); results are bitwise reproducible.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _cases import assert_close, fp16_case, int8_case, oracle_fp16, oracle_int8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GRID, SCHED = 1, 2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib(built):
+    import pa_int8
+
+    pa_int8.ext()
+    yield
+    pa_int8.capi().pa_decode_set_schedule(0)
+
+
+def _mode(m):
+    import pa_int8
+
+    assert pa_int8.capi().pa_decode_set_schedule(m) == 0
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def ragged_lens(n, seed, lo=1, hi=3000):
+    rng = np.random.default_rng(seed)
+    x = np.exp(rng.normal(math.log(300), 1.2, n))
+    return np.clip(np.round(x), lo, hi).astype(np.int32)
+
+
+def run(c, variant, lens=None, bt=None, check=True, int8=False, partition=0):
+    import pa_int8
+
+    q = _t(c["q"])
+    out = torch.empty_like(q)
+    kw = {}
+    if int8:
+        kc, vc, table = c["k_cache8"], c["v_cache8"], c["block_table8"]
+        kw = dict(k_scales=_t(c["k_scales"]), v_scales=_t(c["v_scales"]))
+    else:
+        kc, vc, table = c["k_cache"], c["v_cache"], c["block_table"]
+    pa_int8.decode(variant, out, q, _t(kc), _t(vc), _t(table if bt is None else bt),
+                   _t(c["lens"] if lens is None else lens), c["scale"], c["block_size"],
+                   check=check, partition_tokens=partition, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("variant", ["warp", "splitk"])
+@pytest.mark.parametrize("heads", [(16, 8), (12, 2), (32, 1)])
+def test_ragged_fp16(mode, variant, heads):
+    _mode(mode)
+    lens = ragged_lens(37, seed=heads[1])
+    c = fp16_case(len(lens), lens, heads[0], heads[1], seed=11)
+    assert_close(run(c, variant), oracle_fp16(c), what=f"mode {mode} {variant} {heads}")
+
+
+@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("variant", ["warp_int8", "splitk_int8"])
+@pytest.mark.parametrize("heads", [(16, 8), (32, 1)])
+def test_ragged_int8(mode, variant, heads):
+    _mode(mode)
+    lens = ragged_lens(29, seed=heads[1] + 3)
+    c = int8_case(len(lens), lens, heads[0], heads[1], seed=12)
+    assert_close(run(c, variant, int8=True), oracle_int8(c), what=f"mode {mode} {variant}")
+
+
+@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("variant", ["warp", "splitk"])
+def test_capacity_sized_block_table(mode, variant):
+    """A block table sized for a long maximum length with short sequences in it
+    (the serving layout): the grid plans many empty splits, the schedule none."""
+    _mode(mode)
+    lens = ragged_lens(20, seed=5, hi=900)
+    c = fp16_case(len(lens), lens, 8, 2, seed=13)
+    bt = np.zeros((len(lens), c["block_table"].shape[1] * 6), np.int32)
+    bt[:, :c["block_table"].shape[1]] = c["block_table"]
+    assert_close(run(c, variant, bt=bt), oracle_fp16(c), what=f"mode {mode} {variant}")
+
+
+@pytest.mark.parametrize("num_seqs", [1024, 1025])
+@pytest.mark.parametrize("variant", ["warp", "splitk"])
+def test_many_sequences(num_seqs, variant):
+    """The in-kernel schedule holds up to 1024 sequences; 1025 falls back to the grid."""
+    _mode(0)
+    rng = np.random.default_rng(num_seqs)
+    lens = rng.integers(1, 80, size=num_seqs).astype(np.int32)
+    c = fp16_case(num_seqs, lens, 4, 1, head_dim=64, seed=14)
+    assert_close(run(c, variant), oracle_fp16(c), what=f"{num_seqs} seqs")
+    _mode(SCHED)
+    assert_close(run(c, variant), oracle_fp16(c), what=f"{num_seqs} seqs, schedule forced")
+
+
+@pytest.mark.parametrize("variant", ["warp", "splitk", "warp_int8", "splitk_int8"])
+def test_schedule_is_reproducible(variant):
+    _mode(SCHED)
+    lens = ragged_lens(33, seed=21)
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, 16, 4, seed=15)
+    a = run(c, variant, int8=int8)
+    for _ in range(3):
+        assert np.array_equal(run(c, variant, int8=int8), a)
+
+
+def test_claim_counters_reset_between_shapes():
+    """Different shapes and lengths back to back on one stream: every launch
+    must see zeroed claim and arrival counters."""
+    _mode(SCHED)
+    for i, (n, heads, hi) in enumerate([(9, (8, 2), 4000), (40, (16, 8), 600),
+                                        (3, (32, 1), 9000), (64, (8, 2), 200)]):
+        lens = ragged_lens(n, seed=40 + i, hi=hi)
+        c = fp16_case(n, lens, heads[0], heads[1], seed=16 + i)
+        for variant in ("warp", "splitk"):
+            assert_close(run(c, variant), oracle_fp16(c), what=f"shape {i} {variant}")
+
+
+@pytest.mark.parametrize("variant", ["warp", "splitk"])
+def test_schedule_zero_and_clamped_context(variant):
+    """No-check entry under the schedule: ctx <= 0 gives zeros, ctx beyond the
+    block table is clamped to it."""
+    _mode(SCHED)
+    c = fp16_case(4, np.array([40, 20, 33, 500], dtype=np.int32), 8, 2, seed=17)
+    lens = np.array([0, 20, 10_000, -3], dtype=np.int32)
+    got = run(c, variant, lens=lens, check=False)
+    assert np.all(got[0] == 0) and np.all(got[3] == 0)
+    cap = c["block_table"].shape[1] * c["block_size"]
+    c2 = dict(c, lens=np.array([1, 20, cap, 1], dtype=np.int32))
+    assert_close(got[1:3], oracle_fp16(c2)[1:3], what="clamped")
+
+
+@pytest.mark.parametrize("partition", [64, 320, 2048])
+def test_schedule_forced_partition(partition):
+    _mode(SCHED)
+    lens = ragged_lens(12, seed=partition, hi=5000)
+    c = fp16_case(len(lens), lens, 12, 2, seed=18)
+    for variant in ("warp", "splitk"):
+        assert_close(run(c, variant, partition=partition), oracle_fp16(c),
+                     what=f"P={partition} {variant}")
