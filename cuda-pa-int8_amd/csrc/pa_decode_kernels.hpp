@@ -59,6 +59,9 @@ constexpr float kNegInf = -INFINITY;
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -105,114 +108,72 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
   return make_uint4(d[0], d[1], d[2], d[3]);
 }
 
-// LDS of the split merge: weights of up to 64 splits at a time, per head.
-struct MergeSmem {
-  float w[64][16];
-  float inv_l[16];
-};
+// Buffer resource over [base, base + bytes).  The base must be uniform over
+// the wave (it lives in scalar registers); offsets past `bytes` read zeros and
+// drop writes.
+constexpr int kBufWord3 = 0x00020000;   // 32-bit data format, raw (untyped) access
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufWord3);
+}
+// Cache policy of buffer accesses: device-coherent (sc1) stores write
+// through to memory, device-coherent loads do not hit in a stale L2 line; the
+// same bits the compiler uses for agent-scope atomic loads and stores.
+constexpr int kPolicyDevice = 16;
 
 // Merge the `ns` partials of one unit (gt heads) and write its fp16 output
 // rows.  The partial of split sp sits in slot slot0 + sp * stride: acc[gt][D]
-// (relative to m), and (m, l) per head.
-// COHERENT: read with device-coherent loads (partials written in this launch).
-// Loads are issued in independent batches so the merge costs a few memory
-// round trips, not one per split.  Called by every thread of the work-group.
+// (relative to its max) and (m, l) per head.  Thread i owns (head, 4-dim
+// chunk) items i, i + THREADS, ... and merges them without LDS or barriers:
+// the (m, l) pairs and accumulators of 8 splits at a time are loaded in one
+// batch and folded into a running (max, sum, acc).
+// COHERENT: device-coherent loads (partials written in this launch).
 template <int D, int THREADS, bool COHERENT>
-__device__ __forceinline__ void merge_partials(const float* __restrict__ pacc,
-                                               const float* __restrict__ pml,
-                                               half_t* __restrict__ out, size_t slot0, int stride,
-                                               int gt, size_t out_base, int ns, MergeSmem& msm) {
-  constexpr int PER = (16 * D + THREADS - 1) / THREADS;
-  constexpr int SB = PER >= 16 ? 1 : 16 / PER;   // splits per batch: 16 loads in flight per thread
-  auto ld = [](const float* p) -> float {
-    if constexpr (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *p;
-  };
+__device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
+                                             const float* __restrict__ pml,
+                                             half_t* __restrict__ out, size_t slot0, int stride,
+                                             int gt, size_t out_base, int ns) {
+  constexpr int CH = D / 4;
+  constexpr int SB = 8;
+  constexpr int POL = COHERENT ? kPolicyDevice : 0;
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));   // nothing lane-dependent is hoisted out of a caller's loop
-  // Accumulator loads of one batch of SB splits (zeros past the end).
-  float v[SB][PER];
-  auto load_batch = [&](int sb, int se) {
+  const int nitems = gt * CH;
+  const uint32_t acc_bytes = (uint32_t)(gt * D * 4), ml_bytes = (uint32_t)(gt * 8);
+  for (int i = tid; i < nitems; i += THREADS) {
+    const int h = i / CH, c = i - h * CH;
+    float M = kNegInf, L = 0.f;
+    f4_t A = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ns; s0 += SB) {
+      f4_t v[SB];
+      f2_t ml[SB];
 #pragma unroll
-    for (int u = 0; u < SB; ++u)
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int idx = tid + i * THREADS;
-        const int hh = idx / D, d = idx - hh * D;
-        const int sp = sb + u;
-        v[u][i] = (sp < se && hh < gt) ? ld(pacc + ((slot0 + (size_t)sp * stride) * gt + hh) * D + d) : 0.f;
+      for (int u = 0; u < SB; ++u) {
+        // Past the last split the last one is re-read (and weighted 0), so
+        // every load of the batch is unconditional.
+        const size_t slot = slot0 + (size_t)min(s0 + u, ns - 1) * stride;
+        const auto ra = buf_rsrc(pacc + slot * gt * D, acc_bytes);
+        const auto rm = buf_rsrc(pml + slot * gt * 2, ml_bytes);
+        v[u] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * c) * 4, 0, POL));
+        ml[u] = __builtin_bit_cast(f2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, 0, POL));
       }
-  };
-  // The first batch goes out with the (m, l) loads: one round trip for both.
-  load_batch(0, min(ns, 64));
-  // Per head h: 16 threads (one DPP row) own the splits k, k+16, k+32, ...
-  const int h = tid >> 4, k = tid & 15;
-  const bool hv = h < gt;
-  float mv[4], lv[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int sp = k + 16 * u;
-    const bool ok = hv && sp < ns;
-    const size_t pi = (slot0 + (size_t)sp * stride) * gt + h;
-    mv[u] = ok ? ld(pml + pi * 2) : kNegInf;
-    lv[u] = ok ? ld(pml + pi * 2 + 1) : 0.f;
-  }
-  float mx = kNegInf;
-  for (int sp = k + 64; hv && sp < ns; sp += 16) mx = fmaxf(mx, ld(pml + ((slot0 + (size_t)sp * stride) * gt + h) * 2));
-#pragma unroll
-  for (int u = 0; u < 4; ++u) mx = fmaxf(mx, mv[u]);
-  mx = fmaxf(mx, dpp_mov<kQuadXor1>(mx));
-  mx = fmaxf(mx, dpp_mov<kQuadXor2>(mx));
-  mx = fmaxf(mx, dpp_mov<kRowHalfMirror>(mx));
-  mx = fmaxf(mx, dpp_mov<kRowMirror>(mx));
-  float l = 0.f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) l += mv[u] == kNegInf ? 0.f : lv[u] * exp2f_fast(mv[u] - mx);
-  for (int sp = k + 64; hv && sp < ns; sp += 16) {
-    const size_t pi = (slot0 + (size_t)sp * stride) * gt + h;
-    const float m_s = ld(pml + pi * 2);
-    if (m_s != kNegInf) l += ld(pml + pi * 2 + 1) * exp2f_fast(m_s - mx);
-  }
-  l += dpp_mov<kQuadXor1>(l);
-  l += dpp_mov<kQuadXor2>(l);
-  l += dpp_mov<kRowHalfMirror>(l);
-  l += dpp_mov<kRowMirror>(l);
-  if (k == 0 && hv) msm.inv_l[h] = l > 0.f ? 1.f / l : 0.f;
-  float a[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) a[i] = 0.f;
-  for (int s0 = 0; s0 < ns; s0 += 64) {
-    const int se = min(ns, s0 + 64);
-    __syncthreads();
-    if (s0 == 0) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (hv && k + 16 * u < ns) msm.w[k + 16 * u][h] = mv[u] == kNegInf ? 0.f : exp2f_fast(mv[u] - mx);
-    } else if (hv) {
-      for (int sp = s0 + k; sp < se; sp += 16) {
-        const float m_s = ld(pml + ((slot0 + (size_t)sp * stride) * gt + h) * 2);
-        msm.w[sp - s0][h] = m_s == kNegInf ? 0.f : exp2f_fast(m_s - mx);
-      }
-    }
-    __syncthreads();
-    for (int sb = s0; sb < se; sb += SB) {
-      if (sb != 0) load_batch(sb, se);
+      float mb = M;
 #pragma unroll
       for (int u = 0; u < SB; ++u)
+        if (s0 + u < ns) mb = fmaxf(mb, ml[u].x);
+      const float fo = M == kNegInf ? 0.f : exp2f_fast(M - mb);
+      A *= fo;
+      L *= fo;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const int hh = (tid + i * THREADS) / D;
-          const int sp = sb + u;
-          if (sp < se && hh < gt) a[i] += v[u][i] * msm.w[sp - s0][hh];
-        }
+      for (int u = 0; u < SB; ++u) {
+        const float f = (s0 + u < ns && ml[u].x != kNegInf) ? exp2f_fast(ml[u].x - mb) : 0.f;
+        A += v[u] * f;
+        L += ml[u].y * f;
+      }
+      M = mb;
     }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int idx = tid + i * THREADS;
-    const int hh = idx / D, d = idx - hh * D;
-    if (hh < gt) out[out_base + (size_t)hh * D + d] = (half_t)(a[i] * msm.inv_l[hh]);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const uint2 pk = make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
+    *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
   }
 }
 
@@ -223,14 +184,21 @@ constexpr int split_blocks_max() {
   return kMaxPartitionPer4Waves * NW / 4 / kMinBlockSize + 1;
 }
 
+// Row padding of the wave-merge slots: lane (r, g) touches row r, so rows
+// D floats apart would put the 16 lanes of one g on the same LDS banks.
+constexpr int kMergeRowPad = 4;
+// Occupancy the decode kernels are built for: 2 waves per SIMD, so 8 waves
+// (one 8-wave or two 4-wave work-groups) share a CU's 160 KB of LDS.
+constexpr int kWavesPerCU = 8;
+constexpr size_t kLdsPerCU = 160 * 1024 - 4096;   // (margin for allocation granularity)
+
 template <int D, int NW>
 struct alignas(16) DecodeSmem {
-  float a[NW / 2][16][D];   // merge slots: per head, per dim
-  float m[NW / 2][16];
-  float l[NW / 2][16];
-  int blk[split_blocks_max<NW>()];   // the split's block ids
+  float a[NW][16][D + kMergeRowPad];   // each wave's accumulator: per head, per dim (+ pad)
+  float m[NW][16];
+  float l[NW][16];
+  int blk[split_blocks_max<NW>()];     // the split's block ids
   int last;
-  MergeSmem merge;
 };
 
 // One split of one unit, processed by a whole work-group.
@@ -563,69 +531,55 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] *= unscale;
 
-  // ---- merge the NW waves pairwise through LDS: [NW/2, NW) -> [0, NW/2), ...
-#pragma unroll
-  for (int half = NW / 2; half >= 1; half /= 2) {
-    if (w >= half && w < 2 * half) {
-      const int slot = w - half;
-      if (g == 0) {
-        sm.m[slot][r] = m_run;
-        sm.l[slot][r] = l_run;
-      }
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        *reinterpret_cast<f4_t*>(&sm.a[slot][r][16 * t + 4 * g]) = acc[t];
+  // ---- every wave's state goes to LDS; then each thread merges the NW
+  // states of its (head, 4-dim chunk) items and writes them out: the output
+  // when the unit has one split, else this split's partial.
+  if (r < gt) {
+    if (g == 0) {
+      sm.m[w][r] = m_run;
+      sm.l[w][r] = l_run;
     }
-    __syncthreads();
-    if (w < half) {
-      const float m2 = sm.m[w][r], l2 = sm.l[w][r];
-      const float mx = fmaxf(m_run, m2);
-      const float f1 = m_run == kNegInf ? 0.f : exp2f_fast(m_run - mx);
-      const float f2 = m2 == kNegInf ? 0.f : exp2f_fast(m2 - mx);
-      l_run = l_run * f1 + l2 * f2;
-      m_run = mx;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[t] = acc[t] * f1 + *reinterpret_cast<const f4_t*>(&sm.a[w][r][16 * t + 4 * g]) * f2;
-    }
-    __syncthreads();
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<f4_t*>(&sm.a[w][r][16 * t + 4 * g]) = acc[t];
   }
+  __syncthreads();
 
-  // ---- wave 0 holds the work-group result
+  constexpr int CH = D / 4;
   const size_t out_base = ((size_t)seq * sh.num_heads + head0) * D;
   const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
-  if (w == 0 && r < gt) {
+  const size_t slot = wk.slot0 + (size_t)split * wk.stride;
+  const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
+  const auto rml = buf_rsrc(pml + slot * gt * 2, (uint32_t)(gt * 8));
+  for (int i = tid; i < gt * CH; i += NW * kWave) {
+    const int h = i / CH, c = i - h * CH;
+    float mw[NW], M = kNegInf;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      mw[v] = sm.m[v][h];
+      M = fmaxf(M, mw[v]);
+    }
+    f4_t A = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float f = mw[v] == kNegInf ? 0.f : exp2f_fast(mw[v] - M);
+      L += sm.l[v][h] * f;
+      A += *reinterpret_cast<const f4_t*>(&sm.a[v][h][4 * c]) * f;
+    }
     if (final_here) {
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const f4_t v = acc[t] * inv;
-        const uint2 pk = make_uint2(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]));
-        *reinterpret_cast<uint2*>(out + out_base + (size_t)r * D + 16 * t + 4 * g) = pk;
-      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const uint2 pk = make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
+      *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
     } else {
-      const size_t pi = (wk.slot0 + (size_t)split * wk.stride) * gt + r;
-      float* pa = pacc + pi * D + 4 * g;
-      if constexpr (FUSED) {
-        // Device-coherent (write-through) stores: visible to every XCD once
-        // this thread's stores are acknowledged.
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            __hip_atomic_store(pa + 16 * t + e, acc[t][e], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        if (g == 0) {
-          __hip_atomic_store(pml + pi * 2, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(pml + pi * 2 + 1, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) *reinterpret_cast<f4_t*>(pa + 16 * t) = acc[t];
-        if (g == 0) {
-          pml[pi * 2] = m_run;
-          pml[pi * 2 + 1] = l_run;
-        }
+      // FUSED: device-coherent (write-through) stores, visible to every XCD
+      // once this thread's stores are acknowledged.
+      constexpr int POL = FUSED ? kPolicyDevice : 0;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc,
+                                             (h * D + 4 * c) * 4, 0, POL);
+      if (c == 0) {
+        const f2_t ml = {M, L};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml), rml, h * 8, 0, POL);
       }
     }
   }
@@ -644,8 +598,8 @@ __device__ __forceinline__ void decode_split(
       }
       __syncthreads();
       if (sm.last) {
-        merge_partials<D, NW * kWave, true>(pacc, pml, out, wk.slot0, wk.stride, gt, out_base,
-                                            ns_eff, sm.merge);
+        merge_splits<D, NW * kWave, true>(pacc, pml, out, wk.slot0, wk.stride, gt, out_base,
+                                          ns_eff);
         if (threadIdx.x == 0)
           __hip_atomic_store(cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -661,7 +615,7 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
               const float* __restrict__ vsc, const int* __restrict__ bt,
               const int* __restrict__ ctxl, half_t* __restrict__ out, float* __restrict__ pacc,
               float* __restrict__ pml, uint32_t* __restrict__ cnt, DecodeShape sh) {
-  static_assert(sizeof(DecodeSmem<D, NW>) <= 64 * 1024, "LDS budget");
+  static_assert(sizeof(DecodeSmem<D, NW>) * (kWavesPerCU / NW) <= kLdsPerCU, "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
 
   // ---- work item (XCD-aware: the head chunks of one item share blockIdx % 8)
@@ -720,7 +674,7 @@ struct SchedArgs {
 struct SchedSmem {
   int full_pre[kSchedMaxSeqs + 1];   // exclusive prefix of full rows per sequence
   int part_pre[kSchedMaxSeqs + 1];   // exclusive prefix of short last rows
-  int ctx[kSchedMaxSeqs];
+  uint16_t rem[kSchedMaxSeqs];       // context length % P (P <= 8192)
   uint32_t red[3][16];               // per-wave sum (in 1024-token units), min, max
   int scan_f[16], scan_p[16];
   int next_item;
@@ -792,7 +746,6 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
       tk += (uint32_t)v >> 10;   // the total only steers the partition choice
       mn = mn < (uint32_t)v ? mn : (uint32_t)v;
       mx = mx > (uint32_t)v ? mx : (uint32_t)v;
-      ss.ctx[i] = v;
     }
   }
   tk = wave_reduce_u(tk, OpAddU());
@@ -866,6 +819,7 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
       if (i < S) {
         ss.full_pre[i] = fo;
         ss.part_pre[i] = po;
+        ss.rem[i] = (uint16_t)(c[e] % P);
         fo += c[e] / P;
         po += (c[e] % P != 0 || c[e] == 0) ? 1 : 0;
       }
@@ -890,7 +844,8 @@ decode_sched_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc
                     const int* __restrict__ ctxl, half_t* __restrict__ out,
                     float* __restrict__ pacc, float* __restrict__ pml, uint32_t* __restrict__ cnt,
                     DecodeShape sh, SchedArgs sa) {
-  static_assert(sizeof(DecodeSmem<D, NW>) + sizeof(SchedSmem) <= 64 * 1024, "LDS budget");
+  static_assert((sizeof(DecodeSmem<D, NW>) + sizeof(SchedSmem)) * (kWavesPerCU / NW) <= kLdsPerCU,
+                "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
   __shared__ SchedSmem ss;
   const Schedule sc = build_schedule<NW * kWave>(ctxl, sh, sa, ss);
@@ -935,7 +890,10 @@ decode_sched_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc
     const int ns = __builtin_amdgcn_readfirstlane(
         (ss.full_pre[seq + 1] - ss.full_pre[seq]) + (ss.part_pre[seq + 1] - ss.part_pre[seq]));
     const int rowbase = __builtin_amdgcn_readfirstlane(ss.full_pre[seq] + ss.part_pre[seq]);
-    const int ctx = __builtin_amdgcn_readfirstlane(ss.ctx[seq]);
+    // A full row ends at its partition boundary, a short last row at the
+    // sequence's length.
+    const int ctx = row < n_full ? (split + 1) * P
+                                 : split * P + __builtin_amdgcn_readfirstlane((int)ss.rem[seq]);
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
     decode_split<D, NW, I8, FUSED, true>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
@@ -965,7 +923,6 @@ __global__ void __launch_bounds__(kThreads)
 sched_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
                     const int* __restrict__ ctxl, const int* __restrict__ info,
                     half_t* __restrict__ out, DecodeShape sh, int rows_max) {
-  __shared__ MergeSmem msm;
   const int unit = blockIdx.x;
   const int chunk = unit % sh.nchunk;
   const int sk = unit / sh.nchunk;
@@ -982,9 +939,9 @@ sched_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pm
   if (rb < 0 || rb > rows_max - ns) return;   // slots stay inside the partial buffers
   const size_t rowbase = (size_t)rb;
   const int head0 = kvh * sh.group + chunk * sh.head_tile;
-  merge_partials<D, kThreads, false>(
+  merge_splits<D, kThreads, false>(
       pacc, pml, out, (rowbase * sh.num_kv_heads + kvh) * sh.nchunk + chunk,
-      sh.num_kv_heads * sh.nchunk, sh.head_tile, ((size_t)seq * sh.num_heads + head0) * D, ns, msm);
+      sh.num_kv_heads * sh.nchunk, sh.head_tile, ((size_t)seq * sh.num_heads + head0) * D, ns);
 }
 
 // Split-K reduce: one work-group per (seq, kv_head, head chunk).
@@ -992,7 +949,6 @@ template <int D>
 __global__ void __launch_bounds__(kThreads)
 splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
                      const int* __restrict__ ctxl, half_t* __restrict__ out, DecodeShape sh) {
-  __shared__ MergeSmem msm;
   const int unit = blockIdx.x;
   const int chunk = unit % sh.nchunk;
   const int sk = unit / sh.nchunk;
@@ -1003,8 +959,8 @@ splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ p
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
   const int head0 = kvh * sh.group + chunk * sh.head_tile;
-  merge_partials<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, 1, sh.head_tile,
-                                     ((size_t)seq * sh.num_heads + head0) * D, ns_eff, msm);
+  merge_splits<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, 1, sh.head_tile,
+                                   ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
 }
 
 template <int D, int NW, bool I8>
