@@ -53,11 +53,19 @@ at::Tensor workspace_for(const at::Tensor& like, hipStream_t stream, size_t byte
 
 void check_status(pa_status_t st) { TORCH_CHECK(st == PA_OK, pa_status_string(st)); }
 
+// Which reference launcher's block_size rule an op repeats: the naive stage
+// checks none (paged_attention_naive.cu:135-140), the vectorised stage only a
+// multiple of 8 (paged_attention_v1_vectorized.cu:124), the later ones also
+// that it divides the 128-token tile (v2_online.cu:157, v3_warp.cu:149-150).
+// The library's own rule (pa_validate_decode) applies to every op after it.
+enum class BlockRule { kNone, kMultipleOf8, kTile };
+
 void run_decode(pa_decode_kind_t kind, at::Tensor& out, const at::Tensor& q,
                 const at::Tensor& k_cache, const at::Tensor& v_cache,
                 const at::Tensor* k_scales, const at::Tensor* v_scales,
                 const at::Tensor& block_table, const at::Tensor& context_lens, double scale,
-                int64_t block_size, bool check_context, int64_t partition_tokens) {
+                int64_t block_size, bool check_context, int64_t partition_tokens,
+                BlockRule rule = BlockRule::kTile) {
   const bool int8 = kind == PA_DECODE_WARP_I8 || kind == PA_DECODE_SPLITK_I8;
   // The reference launchers' checks, in their order (paged_attention_v3_warp.cu:143-150,
   // paged_attention_v5_warp_int8.cu:159-168).
@@ -87,9 +95,11 @@ void run_decode(pa_decode_kind_t kind, at::Tensor& out, const at::Tensor& q,
   if (int8) {
     TORCH_CHECK(block_size % 16 == 0 && kRefTile % block_size == 0,
                 "block_size must divide TILE and be a multiple of 16");
-  } else {
+  } else if (rule == BlockRule::kTile) {
     TORCH_CHECK(block_size % 8 == 0 && kRefTile % block_size == 0,
                 "block_size must divide TILE and be a multiple of 8");
+  } else if (rule == BlockRule::kMultipleOf8) {
+    TORCH_CHECK(block_size % 8 == 0, "block_size must be a multiple of 8 for vectorized V");
   }
   // Layout checks the reference leaves implicit.
   TORCH_CHECK(q.dim() == 3 && out.sizes() == q.sizes() && out.scalar_type() == at::kHalf,
@@ -169,8 +179,31 @@ void run_decode(pa_decode_kind_t kind, at::Tensor& out, const at::Tensor& q,
   check_status(st);
 }
 
-// ---- the reference's six-op surface (kernels/bindings.cpp:7-43), minus the
-// ---- vec/online ladder stages that are not part of this path
+// ---- the reference's six-op surface (kernels/bindings.cpp:7-43) and the naive
+// ---- op of its second module (paged_attention_naive.cu:169-172).  The ladder
+// ---- stages naive / vec / online compute the same function as warp; on gfx950
+// ---- one single-launch kernel serves all four, behind each stage's own checks.
+
+void paged_decode_attention(at::Tensor out, at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
+                            at::Tensor block_table, at::Tensor context_lens, double scale,
+                            int64_t block_size) {
+  run_decode(PA_DECODE_WARP_F16, out, q, k_cache, v_cache, nullptr, nullptr, block_table,
+             context_lens, scale, block_size, true, 0, BlockRule::kNone);
+}
+
+void paged_decode_attn_vec(at::Tensor out, at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
+                           at::Tensor block_table, at::Tensor context_lens, double scale,
+                           int64_t block_size) {
+  run_decode(PA_DECODE_WARP_F16, out, q, k_cache, v_cache, nullptr, nullptr, block_table,
+             context_lens, scale, block_size, true, 0, BlockRule::kMultipleOf8);
+}
+
+void paged_decode_attn_online(at::Tensor out, at::Tensor q, at::Tensor k_cache,
+                              at::Tensor v_cache, at::Tensor block_table,
+                              at::Tensor context_lens, double scale, int64_t block_size) {
+  run_decode(PA_DECODE_WARP_F16, out, q, k_cache, v_cache, nullptr, nullptr, block_table,
+             context_lens, scale, block_size, true, 0, BlockRule::kTile);
+}
 
 void paged_decode_attn_warp(at::Tensor out, at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
                             at::Tensor block_table, at::Tensor context_lens, double scale,
@@ -274,6 +307,13 @@ void reshape_and_cache_int8(at::Tensor key, at::Tensor value, at::Tensor k_cache
 }  // namespace
 
 PYBIND11_MODULE(paged_attn_opt, m) {
+  m.def("paged_decode_attention", &paged_decode_attention,
+        "paged decode (FP16 KV), the naive stage's entry name; single-launch kernel, gfx950");
+  m.def("paged_decode_attn_vec", &paged_decode_attn_vec,
+        "paged decode (FP16 KV), the vectorized stage's entry name; single-launch kernel, gfx950");
+  m.def("paged_decode_attn_online", &paged_decode_attn_online,
+        "paged decode (FP16 KV), the online-softmax stage's entry name; single-launch kernel, "
+        "gfx950");
   m.def("paged_decode_attn_warp", &paged_decode_attn_warp,
         "single-launch paged decode (FP16 KV), gfx950");
   m.def("paged_decode_attn_splitk", &paged_decode_attn_splitk,

@@ -10,8 +10,10 @@ reference:
   block_table, context_lens, scale, block_size=16) -> out`` for
   ``"warp_int8"`` and ``"splitk_int8"``.
 
-The ladder stages ``naive``, ``vec`` and ``online`` of the reference are not
-part of this path and are not registered.
+The ladder stages ``naive``, ``vec`` and ``online`` (the reference's
+optimisation history of the same function) are registered under their names
+too, each with its launcher's block_size rule; on gfx950 the single-launch
+kernel serves them.
 
 Additions: ``decode`` (any variant, optional host check, forced partition
 size), ``decode_plan`` and ``reshape_and_cache_int8`` (the new quantize +
@@ -48,7 +50,20 @@ def _make_variant_int8(op_name):
     return run
 
 
+def paged_decode_attention(out, q, k_cache, v_cache, block_table, context_lens, scale,
+                           block_size=16):
+    """The reference's top-level entry name (tests/cuda_ext.py:104-109, the
+    naive stage of paged_attention_naive.cu:125-167), served by the
+    single-launch kernel."""
+    _ext().paged_decode_attention(out, q, k_cache, v_cache, block_table, context_lens,
+                                  float(scale), int(block_size))
+    return out
+
+
 VARIANTS = {
+    "naive": paged_decode_attention,
+    "vec": _make_variant("paged_decode_attn_vec"),
+    "online": _make_variant("paged_decode_attn_online"),
     "warp": _make_variant("paged_decode_attn_warp"),
     "splitk": _make_variant("paged_decode_attn_splitk"),
 }
@@ -56,14 +71,6 @@ VARIANTS_INT8 = {
     "warp_int8": _make_variant_int8("paged_decode_attn_warp_int8"),
     "splitk_int8": _make_variant_int8("paged_decode_attn_splitk_int8"),
 }
-
-
-def paged_decode_attention(out, q, k_cache, v_cache, block_table, context_lens, scale,
-                           block_size=16):
-    """The reference's top-level entry name (tests/cuda_ext.py:104-109), served
-    by the single-launch kernel."""
-    return VARIANTS["warp"](out, q, k_cache, v_cache, block_table, context_lens, scale,
-                            block_size)
 
 
 def decode(variant, out, q, k_cache, v_cache, block_table, context_lens, scale, block_size=16,

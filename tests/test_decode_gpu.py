@@ -66,6 +66,46 @@ def run_int8(c, variant, check=True, partition=0):
 
 # ---------------------------------------------------------------- FP16 matrix
 
+@pytest.mark.parametrize("name", ["naive", "vec", "online", "warp", "splitk"])
+@pytest.mark.parametrize("clen", CONTEXT_LENS)
+@pytest.mark.parametrize("num_heads,num_kv_heads", GQA)
+def test_registry_variant_matches_oracle(name, clen, num_heads, num_kv_heads):
+    """Every name of the reference registry (tests/cuda_ext.py:112-125), called
+    with its own signature, as tests/test_paged_decode_attn.py:80-119 does."""
+    import pa_int8
+
+    c = fp16_case(3, make_lens(clen, 3), num_heads, num_kv_heads, seed=21)
+    q = _t(c["q"])
+    out = torch.empty_like(q)
+    ret = pa_int8.VARIANTS[name](out, q, _t(c["k_cache"]), _t(c["v_cache"]),
+                                 _t(c["block_table"]), _t(c["lens"]), c["scale"],
+                                 c["block_size"])
+    assert ret is out
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy(), oracle_fp16(c), what=name)
+
+
+def test_registry_block_size_rules():
+    """vec accepts any multiple of 8 the library builds (paged_attention_v1_vectorized.cu:124);
+    online / warp / splitk also require it to divide the 128-token tile
+    (v2_online.cu:157); sizes outside the library's set raise RuntimeError."""
+    import pa_int8
+
+    c = fp16_case(2, make_lens(100, 2), 8, 2, block_size=8, seed=4)
+    args = lambda: (torch.empty_like(_t(c["q"])), _t(c["q"]), _t(c["k_cache"]),  # noqa: E731
+                    _t(c["v_cache"]), _t(c["block_table"]), _t(c["lens"]), c["scale"])
+    for name in ("naive", "vec", "online", "warp", "splitk"):
+        out = pa_int8.VARIANTS[name](*args(), 8)
+        torch.cuda.synchronize()
+        assert_close(out.float().cpu().numpy(), oracle_fp16(c), what=name)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        pa_int8.VARIANTS["vec"](*args(), 12)
+    with pytest.raises(RuntimeError, match="divide TILE"):
+        pa_int8.VARIANTS["online"](*args(), 24)
+    with pytest.raises(RuntimeError):
+        pa_int8.VARIANTS["naive"](*args(), 12)
+
+
 @pytest.mark.parametrize("variant", F16_VARIANTS)
 @pytest.mark.parametrize("clen", CONTEXT_LENS)
 @pytest.mark.parametrize("num_heads,num_kv_heads", GQA)

@@ -172,11 +172,14 @@ def test_registry_mirrors_reference_names(built):
     import cuda_ext
     import pa_int8
 
-    assert set(cuda_ext.VARIANTS) == {"warp", "splitk"}
+    # tests/cuda_ext.py:38-49,112-141
+    assert set(cuda_ext.VARIANTS) == {"naive", "vec", "online", "warp", "splitk"}
     assert set(cuda_ext.VARIANTS_INT8) == {"warp_int8", "splitk_int8"}
-    p16 = list(inspect.signature(pa_int8.VARIANTS["warp"]).parameters)
-    assert p16 == ["out", "q", "k_cache", "v_cache", "block_table", "context_lens", "scale",
-                   "block_size"]
+    for name, fn in pa_int8.VARIANTS.items():
+        p16 = list(inspect.signature(fn).parameters)
+        assert p16 == ["out", "q", "k_cache", "v_cache", "block_table", "context_lens", "scale",
+                       "block_size"], name
+    assert cuda_ext.paged_decode_attention is pa_int8.VARIANTS["naive"]
     p8 = list(inspect.signature(pa_int8.VARIANTS_INT8["splitk_int8"]).parameters)
     assert p8 == ["out", "q", "k_cache", "v_cache", "k_scales", "v_scales", "block_table",
                   "context_lens", "scale", "block_size"]
@@ -195,3 +198,15 @@ def test_byte_model_closed_forms():
                                 scales=True) == 2_214_985_760
     assert metrics.quant_write_bytes(64 * 8192, 2, 128) == 817_889_280
     assert metrics.decode_kv_bytes([4096] * 32, 2, 128) == 134_217_728
+
+
+def test_extension_exports_reference_op_names(built):
+    """The six ops of kernels/bindings.cpp:45-58 plus the naive module's
+    paged_decode_attention (paged_attention_naive.cu:169-172)."""
+    import pa_int8
+
+    ext = pa_int8.ext()
+    for op in ("paged_decode_attn_vec", "paged_decode_attn_online", "paged_decode_attn_warp",
+               "paged_decode_attn_splitk", "paged_decode_attn_warp_int8",
+               "paged_decode_attn_splitk_int8", "paged_decode_attention"):
+        assert callable(getattr(ext, op)), op
