@@ -370,29 +370,45 @@ pa_status_t pa_paged_decode_attn_splitk_int8(
                        partition_tokens, workspace, workspace_bytes, stream);
 }
 
-pa_status_t pa_reshape_and_cache_int8(const void* key, const void* value,
-                                      int64_t key_token_stride, int64_t key_head_stride,
-                                      int64_t value_token_stride, int64_t value_head_stride,
-                                      const int64_t* slot_mapping, int32_t num_tokens,
-                                      int32_t num_kv_heads, int32_t head_dim, void* k_cache,
-                                      void* v_cache, float* k_scales, float* v_scales,
-                                      int32_t num_blocks, int32_t block_size, int32_t x,
-                                      pa_stream_t stream) {
-  if (block_size <= 0 || block_size % 16 != 0 || kRefTile % block_size != 0)
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the cache-write entry points: 16-byte row loads and row
+// stores need 16-byte aligned rows and bases.
+pa_status_t check_write_args(const void* key, const void* value, int64_t kts, int64_t khs,
+                             int64_t vts, int64_t vhs, const int64_t* slot_mapping,
+                             int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                             const void* k_cache, const void* v_cache, int32_t num_blocks,
+                             int32_t block_size, int32_t x, int32_t block_mult) {
+  if (block_size <= 0 || block_size % block_mult != 0 || kRefTile % block_size != 0)
     return PA_ERR_BAD_BLOCK_SIZE;
   if (x != 8 || !supported_head_dim(head_dim)) return PA_ERR_UNSUPPORTED;
   if (num_tokens < 0 || num_kv_heads < 1 || num_blocks < 1) return PA_ERR_BAD_SHAPE;
   if (num_tokens == 0) return PA_OK;
-  if (!key || !value || !slot_mapping || !k_cache || !v_cache || !k_scales || !v_scales)
-    return PA_ERR_NULL_POINTER;
-  // 16-byte row loads and V row stores need 16-byte aligned rows.
-  const int64_t strides[4] = {key_token_stride, key_head_stride, value_token_stride,
-                              value_head_stride};
+  if (!key || !value || !slot_mapping || !k_cache || !v_cache) return PA_ERR_NULL_POINTER;
+  const int64_t strides[4] = {kts, khs, vts, vhs};
   for (int64_t s : strides)
     if (s < 0 || s % 8 != 0) return PA_ERR_BAD_SHAPE;
   const void* ptrs[4] = {key, value, k_cache, v_cache};
   for (const void* p : ptrs)
     if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return PA_ERR_BAD_SHAPE;
+  return PA_OK;
+}
+
+pa_status_t quant_write(const void* key, const void* value, int64_t key_token_stride,
+                        int64_t key_head_stride, int64_t value_token_stride,
+                        int64_t value_head_stride, const int64_t* slot_mapping,
+                        int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                        void* k_cache, void* v_cache, float* k_scales, float* v_scales,
+                        const float* k_scale_in, const float* v_scale_in, int32_t num_blocks,
+                        int32_t block_size, int32_t x, pa_stream_t stream) {
+  const pa_status_t st = check_write_args(
+      key, value, key_token_stride, key_head_stride, value_token_stride, value_head_stride,
+      slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache, v_cache, num_blocks, block_size,
+      x, 16);
+  if (st != PA_OK || num_tokens == 0) return st;
+  if (!k_scales || !v_scales) return PA_ERR_NULL_POINTER;
   pa::QuantLaunch l{};
   l.key = key;
   l.value = value;
@@ -408,10 +424,74 @@ pa_status_t pa_reshape_and_cache_int8(const void* key, const void* value,
   l.v_cache = v_cache;
   l.k_scales = k_scales;
   l.v_scales = v_scales;
+  l.k_scale_in = k_scale_in;
+  l.v_scale_in = v_scale_in;
   l.num_blocks = num_blocks;
   l.block_size = block_size;
   l.stream = reinterpret_cast<hipStream_t>(stream);
   return pa::launch_quant_write_i8(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+pa_status_t pa_reshape_and_cache_int8(const void* key, const void* value,
+                                      int64_t key_token_stride, int64_t key_head_stride,
+                                      int64_t value_token_stride, int64_t value_head_stride,
+                                      const int64_t* slot_mapping, int32_t num_tokens,
+                                      int32_t num_kv_heads, int32_t head_dim, void* k_cache,
+                                      void* v_cache, float* k_scales, float* v_scales,
+                                      int32_t num_blocks, int32_t block_size, int32_t x,
+                                      pa_stream_t stream) {
+  return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
+                     value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
+                     v_cache, k_scales, v_scales, nullptr, nullptr, num_blocks, block_size, x,
+                     stream);
+}
+
+pa_status_t pa_reshape_and_cache_int8_static(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim, void* k_cache, void* v_cache,
+    float* k_scales, float* v_scales, const float* k_scale, const float* v_scale,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream) {
+  if (num_tokens > 0 && (!k_scale || !v_scale)) return PA_ERR_NULL_POINTER;
+  return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
+                     value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
+                     v_cache, k_scales, v_scales, k_scale, v_scale, num_blocks, block_size, x,
+                     stream);
+}
+
+pa_status_t pa_reshape_and_cache_f16(const void* key, const void* value,
+                                     int64_t key_token_stride, int64_t key_head_stride,
+                                     int64_t value_token_stride, int64_t value_head_stride,
+                                     const int64_t* slot_mapping, int32_t num_tokens,
+                                     int32_t num_kv_heads, int32_t head_dim, void* k_cache,
+                                     void* v_cache, int32_t num_blocks, int32_t block_size,
+                                     int32_t x, pa_stream_t stream) {
+  const pa_status_t st = check_write_args(
+      key, value, key_token_stride, key_head_stride, value_token_stride, value_head_stride,
+      slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache, v_cache, num_blocks, block_size,
+      x, 8);
+  if (st != PA_OK || num_tokens == 0) return st;
+  pa::CacheWriteLaunch l{};
+  l.key = key;
+  l.value = value;
+  l.key_token_stride = key_token_stride;
+  l.key_head_stride = key_head_stride;
+  l.value_token_stride = value_token_stride;
+  l.value_head_stride = value_head_stride;
+  l.slot_mapping = slot_mapping;
+  l.num_tokens = num_tokens;
+  l.num_kv_heads = num_kv_heads;
+  l.head_dim = head_dim;
+  l.k_cache = k_cache;
+  l.v_cache = v_cache;
+  l.num_blocks = num_blocks;
+  l.block_size = block_size;
+  l.stream = reinterpret_cast<hipStream_t>(stream);
+  return pa::launch_cache_write_f16(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
 
 }  // extern "C"

@@ -93,6 +93,10 @@ struct QuantLaunch {
   void* v_cache;
   float* k_scales;
   float* v_scales;
+  // Per-tensor mode: one given fp32 scale for every K (V) element, read on
+  // the device; both NULL for the per-token mode.
+  const float* k_scale_in;
+  const float* v_scale_in;
   int num_blocks;
   int block_size;
   hipStream_t stream;
@@ -100,5 +104,26 @@ struct QuantLaunch {
 
 // Defined in pa_quant.hip.
 hipError_t launch_quant_write_i8(const QuantLaunch& l);
+
+struct CacheWriteLaunch {
+  const void* key;
+  const void* value;
+  int64_t key_token_stride;
+  int64_t key_head_stride;
+  int64_t value_token_stride;
+  int64_t value_head_stride;
+  const int64_t* slot_mapping;
+  int num_tokens;
+  int num_kv_heads;
+  int head_dim;
+  void* k_cache;
+  void* v_cache;
+  int num_blocks;
+  int block_size;
+  hipStream_t stream;
+};
+
+// Defined in pa_cache_write.hip.
+hipError_t launch_cache_write_f16(const CacheWriteLaunch& l);
 
 }  // namespace pa

@@ -10,6 +10,10 @@
 //     k_cache[blk, h, :, off, :] = q.view(D/8, 8)
 //     v_cache[blk, h, :, off]    = q
 //     scales[blk, h, off]        = scale,   with slot = blk * block_size + off.
+//   per-tensor mode (PagedKVCache "int8_per_tensor",
+//   benchmarks/int8_bridge/paged_cache.py:99-106,140-142): the caller passes
+//   one fp32 scale for all of K and one for all of V (device pointers), and
+//     q_d = int8(clamp(rne(fp32(x_d) / scale), -127, 127)), scale stored per slot.
 //
 // A job is (16 consecutive input tokens, kv head, K or V).  The grid holds as
 // many work-groups as the GPU keeps resident; each wave loops over jobs with a
@@ -79,6 +83,35 @@ __device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow)
   return out;
 }
 
+// The same with a scale given by the caller (per-tensor mode), where the
+// quotient can exceed the int8 range: a product of magnitude >= 127 gives
+// +-127 (the IEEE quotient then exceeds 126.5, the reciprocal being a normal
+// number, so it rounds to >= 127 and clamps there); the rest lies below 127
+// and rounds as above.
+__device__ __forceinline__ uint2 quant_group_fast_sat(uint4 xv, float r, bool& slow) {
+  const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
+  uint32_t bytes[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
+    const float xs[2] = {(float)h.x, (float)h.y};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float y = xs[e] * r;
+      const bool sat = __builtin_fabsf(y) >= 127.f;
+      slow = slow || (!sat && !(__builtin_fabsf(y - __builtin_rintf(y)) < 0.5f - kTieGuard));
+      bytes[2 * k + e] = sat ? (y > 0.f ? 0x7Fu : 0x81u)
+                             : __builtin_bit_cast(uint32_t, y + kRoundMagic);
+    }
+  }
+  uint2 out;
+  out.x = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bytes[3], bytes[2], 0x0c0c0400u),
+                                __builtin_amdgcn_perm(bytes[1], bytes[0], 0x0c0c0400u), 0x05040100u);
+  out.y = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bytes[7], bytes[6], 0x0c0c0400u),
+                                __builtin_amdgcn_perm(bytes[5], bytes[4], 0x0c0c0400u), 0x05040100u);
+  return out;
+}
+
 // The exact path for one 16-B group.
 __device__ __forceinline__ uint2 quant_group_exact(uint4 xv, float s) {
   const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
@@ -101,13 +134,16 @@ struct QuantJob {
   int64_t slot;
 };
 
-template <int D>
+// STATIC: every K element is quantized with *k_scale_in and every V element
+// with *v_scale_in (the per-tensor mode), instead of its token's own scale.
+template <int D, bool STATIC>
 __global__ void __launch_bounds__(kQuantWaves * kWave)
 quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ value, int64_t kts,
                    int64_t khs, int64_t vts, int64_t vhs, const int64_t* __restrict__ slots,
                    int num_tokens, int num_kv_heads, int8_t* __restrict__ kc,
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
-                   int num_blocks, int bs, int njobs) {
+                   int num_blocks, int bs, int njobs, const float* __restrict__ k_scale_in,
+                   const float* __restrict__ v_scale_in) {
   constexpr int JQ = QuantJob<D>::JQ;
   __shared__ __attribute__((aligned(16))) uint8_t tile[kQuantWaves][D * 16];
 
@@ -156,26 +192,35 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     const int64_t slot = tv ? cur.slot : -1;
     const bool sok = slot >= 0 && slot < pool;
 
-    // amax over the token's D values as fp16 magnitude bits (ordered like the
-    // values; a NaN input gives NaN bits above +inf, so the scale becomes NaN
-    // as in torch).
-    u16x2_t am2 = {0, 0};
+    float s;
+    bool s_normal;
+    if constexpr (STATIC) {
+      s = is_v ? v_scale_in[0] : k_scale_in[0];
+      // The saturating fast path needs a normal, finite reciprocal.
+      const float rr = 1.0f / s;
+      s_normal = rr >= 1.17549435e-38f && rr <= 3.40282347e+38f;
+    } else {
+      // amax over the token's D values as fp16 magnitude bits (ordered like the
+      // values; a NaN input gives NaN bits above +inf, so the scale becomes NaN
+      // as in torch).
+      u16x2_t am2 = {0, 0};
 #pragma unroll
-    for (int j = 0; j < JQ; ++j) {
-      const uint32_t wv[4] = {cur.x[j].x, cur.x[j].y, cur.x[j].z, cur.x[j].w};
+      for (int j = 0; j < JQ; ++j) {
+        const uint32_t wv[4] = {cur.x[j].x, cur.x[j].y, cur.x[j].z, cur.x[j].w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2_t, wv[k] & 0x7FFF7FFFu));
+        for (int k = 0; k < 4; ++k)
+          am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2_t, wv[k] & 0x7FFF7FFFu));
+      }
+      uint32_t am = am2[0] > am2[1] ? am2[0] : am2[1];
+      am = rows_umax(am);
+      const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
+      const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
+      s = (float)(half_t)(a / 127.0f);                    // fp16 division, RNE
+      // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
+      // sends the token's elements to the exact path.
+      s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
     }
-    uint32_t am = am2[0] > am2[1] ? am2[0] : am2[1];
-    am = rows_umax(am);
-    const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
-    const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
-    const float s = (float)(half_t)(a / 127.0f);        // fp16 division, RNE
     const float r = 1.0f / s;                           // IEEE reciprocal (inf when s = 0)
-    // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
-    // sends the token's elements to the exact path.
-    const bool s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
 
     const int64_t blk = sok ? slot / bs : 0;
     const int off = sok ? (int)(slot - blk * bs) : 0;
@@ -193,7 +238,8 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
 #pragma unroll
     for (int j = 0; j < JQ; ++j) {
       bool slow = !s_normal;
-      uint2 qj = quant_group_fast(cur.x[j], r, slow);
+      uint2 qj = STATIC ? quant_group_fast_sat(cur.x[j], r, slow)
+                        : quant_group_fast(cur.x[j], r, slow);
       if (__builtin_amdgcn_ballot_w64(slow) != 0) {
         if (slow) qj = quant_group_exact(cur.x[j], s);   // rare: the reference's division
       }
@@ -250,7 +296,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
 
 // Work-groups the GPU holds at once for this kernel: the grid-stride loop is
 // sized to them so that no group starts after the others have finished.
-template <int D>
+template <int D, bool STATIC>
 int resident_groups() {
   static int cache[64] = {0};
   int dev = 0;
@@ -260,7 +306,7 @@ int resident_groups() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quant_write_kernel<D>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quant_write_kernel<D, STATIC>,
                                                      kQuantWaves * kWave, 0) != hipSuccess ||
         per_cu <= 0)
       per_cu = 4;
@@ -269,27 +315,32 @@ int resident_groups() {
   return cache[dev];
 }
 
-template <int D>
+template <int D, bool STATIC>
 static hipError_t launch_quant_d(const QuantLaunch& l) {
   const int tiles = (l.num_tokens + 15) / 16;
   const int njobs = tiles * l.num_kv_heads * 2;
   const int want = (njobs + kQuantWaves - 1) / kQuantWaves;
-  const int grid = std::min(want, resident_groups<D>());
-  quant_write_kernel<D><<<grid, kQuantWaves * kWave, 0, l.stream>>>(
+  const int grid = std::min(want, resident_groups<D, STATIC>());
+  quant_write_kernel<D, STATIC><<<grid, kQuantWaves * kWave, 0, l.stream>>>(
       static_cast<const half_t*>(l.key), static_cast<const half_t*>(l.value), l.key_token_stride,
       l.key_head_stride, l.value_token_stride, l.value_head_stride, l.slot_mapping, l.num_tokens,
       l.num_kv_heads, static_cast<int8_t*>(l.k_cache), static_cast<int8_t*>(l.v_cache),
-      l.k_scales, l.v_scales, l.num_blocks, l.block_size, njobs);
+      l.k_scales, l.v_scales, l.num_blocks, l.block_size, njobs, l.k_scale_in, l.v_scale_in);
   return hipGetLastError();
 }
 
-hipError_t launch_quant_write_i8(const QuantLaunch& l) {
+template <bool STATIC>
+static hipError_t launch_quant(const QuantLaunch& l) {
   switch (l.head_dim) {
-    case 64: return launch_quant_d<64>(l);
-    case 128: return launch_quant_d<128>(l);
-    case 256: return launch_quant_d<256>(l);
+    case 64: return launch_quant_d<64, STATIC>(l);
+    case 128: return launch_quant_d<128, STATIC>(l);
+    case 256: return launch_quant_d<256, STATIC>(l);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_quant_write_i8(const QuantLaunch& l) {
+  return (l.k_scale_in != nullptr) ? launch_quant<true>(l) : launch_quant<false>(l);
 }
 
 }  // namespace pa

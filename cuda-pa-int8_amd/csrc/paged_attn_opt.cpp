@@ -264,43 +264,97 @@ std::pair<int64_t, int64_t> decode_plan(int64_t kind, int64_t num_seqs, int64_t 
   return {part, ns};
 }
 
-// NEW op (no reference counterpart): per-token INT8 quantize + paged write.
-void reshape_and_cache_int8(at::Tensor key, at::Tensor value, at::Tensor k_cache,
-                            at::Tensor v_cache, at::Tensor k_scales, at::Tensor v_scales,
-                            at::Tensor slot_mapping) {
+// Checks shared by the cache-write ops; `int8` selects the cache dtypes and
+// whether scale tensors are passed.
+void check_write(const at::Tensor& key, const at::Tensor& value, const at::Tensor& k_cache,
+                 const at::Tensor& v_cache, const at::Tensor* k_scales,
+                 const at::Tensor* v_scales, const at::Tensor& slot_mapping, bool int8) {
   TORCH_CHECK(key.is_cuda() && value.is_cuda(), "tensors must be on CUDA");
   TORCH_CHECK(key.scalar_type() == at::kHalf && value.scalar_type() == at::kHalf,
               "key and value must be fp16");
-  TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar,
-              "k_cache and v_cache must be int8");
-  TORCH_CHECK(k_scales.scalar_type() == at::kFloat && v_scales.scalar_type() == at::kFloat,
-              "scales must be fp32");
+  if (int8) {
+    TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar,
+                "k_cache and v_cache must be int8");
+    TORCH_CHECK(k_scales->scalar_type() == at::kFloat && v_scales->scalar_type() == at::kFloat,
+                "scales must be fp32");
+  } else {
+    TORCH_CHECK(k_cache.scalar_type() == at::kHalf && v_cache.scalar_type() == at::kHalf,
+                "k_cache and v_cache must be fp16");
+  }
   TORCH_CHECK(slot_mapping.scalar_type() == at::kLong, "slot_mapping must be int64");
   TORCH_CHECK(key.dim() == 3 && value.sizes() == key.sizes(),
               "key and value must be [num_tokens, num_kv_heads, head_dim]");
   TORCH_CHECK(key.stride(2) == 1 && value.stride(2) == 1, "head_dim must be the innermost dim");
-  TORCH_CHECK(k_cache.dim() == 5 && v_cache.dim() == 4 && k_scales.dim() == 3 &&
-                  v_scales.dim() == 3,
-              "cache tensors have the wrong rank");
+  TORCH_CHECK(k_cache.dim() == 5 && v_cache.dim() == 4, "cache tensors have the wrong rank");
   const int64_t T = key.size(0), Hkv = key.size(1), D = key.size(2);
   const int64_t NB = k_cache.size(0), bs = k_cache.size(3), x = k_cache.size(4);
   TORCH_CHECK(k_cache.size(1) == Hkv && k_cache.size(2) * x == D && v_cache.size(0) == NB &&
                   v_cache.size(1) == Hkv && v_cache.size(2) == D && v_cache.size(3) == bs,
               "cache shapes do not match key/value");
-  TORCH_CHECK(k_scales.size(0) == NB && k_scales.size(1) == Hkv && k_scales.size(2) == bs &&
-                  v_scales.sizes() == k_scales.sizes(),
-              "scales must be [blocks, kv_heads, block_size]");
-  TORCH_CHECK(slot_mapping.dim() == 1 && slot_mapping.size(0) == T, "slot_mapping must be [num_tokens]");
-  for (const at::Tensor* t : {&k_cache, &v_cache, &k_scales, &v_scales, &slot_mapping})
+  TORCH_CHECK(slot_mapping.dim() == 1 && slot_mapping.size(0) == T,
+              "slot_mapping must be [num_tokens]");
+  for (const at::Tensor* t : {&k_cache, &v_cache, &slot_mapping})
     TORCH_CHECK(t->is_contiguous() && t->is_cuda() && t->get_device() == key.get_device(),
                 "cache tensors must be contiguous and on key's device");
+  if (int8) {
+    TORCH_CHECK(k_scales->dim() == 3 && k_scales->size(0) == NB && k_scales->size(1) == Hkv &&
+                    k_scales->size(2) == bs && v_scales->sizes() == k_scales->sizes(),
+                "scales must be [blocks, kv_heads, block_size]");
+    for (const at::Tensor* t : {k_scales, v_scales})
+      TORCH_CHECK(t->is_contiguous() && t->is_cuda() && t->get_device() == key.get_device(),
+                  "cache tensors must be contiguous and on key's device");
+  }
+}
+
+// NEW op (no reference counterpart): per-token INT8 quantize + paged write.
+void reshape_and_cache_int8(at::Tensor key, at::Tensor value, at::Tensor k_cache,
+                            at::Tensor v_cache, at::Tensor k_scales, at::Tensor v_scales,
+                            at::Tensor slot_mapping) {
+  check_write(key, value, k_cache, v_cache, &k_scales, &v_scales, slot_mapping, true);
   const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
   check_status(pa_reshape_and_cache_int8(
       key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
-      value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)T, (int32_t)Hkv, (int32_t)D,
-      k_cache.data_ptr(), v_cache.data_ptr(), k_scales.data_ptr<float>(),
-      v_scales.data_ptr<float>(), (int32_t)NB, (int32_t)bs, (int32_t)x,
+      value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)key.size(0),
+      (int32_t)key.size(1), (int32_t)key.size(2), k_cache.data_ptr(), v_cache.data_ptr(),
+      k_scales.data_ptr<float>(), v_scales.data_ptr<float>(), (int32_t)k_cache.size(0),
+      (int32_t)k_cache.size(3), (int32_t)k_cache.size(4), reinterpret_cast<pa_stream_t>(stream)));
+}
+
+// NEW op: INT8 write with one given scale for all K and one for all V
+// (PagedKVCache's per-tensor mode); k_scale / v_scale are 1-element fp32
+// tensors on key's device, read by the kernel (no host sync).
+void reshape_and_cache_int8_static(at::Tensor key, at::Tensor value, at::Tensor k_cache,
+                                   at::Tensor v_cache, at::Tensor k_scales, at::Tensor v_scales,
+                                   at::Tensor slot_mapping, at::Tensor k_scale,
+                                   at::Tensor v_scale) {
+  check_write(key, value, k_cache, v_cache, &k_scales, &v_scales, slot_mapping, true);
+  for (const at::Tensor* t : {&k_scale, &v_scale})
+    TORCH_CHECK(t->numel() == 1 && t->scalar_type() == at::kFloat && t->is_cuda() &&
+                    t->get_device() == key.get_device(),
+                "k_scale and v_scale must be one fp32 value each on key's device");
+  const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
+  hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  check_status(pa_reshape_and_cache_int8_static(
+      key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
+      value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)key.size(0),
+      (int32_t)key.size(1), (int32_t)key.size(2), k_cache.data_ptr(), v_cache.data_ptr(),
+      k_scales.data_ptr<float>(), v_scales.data_ptr<float>(), k_scale.data_ptr<float>(),
+      v_scale.data_ptr<float>(), (int32_t)k_cache.size(0), (int32_t)k_cache.size(3),
+      (int32_t)k_cache.size(4), reinterpret_cast<pa_stream_t>(stream)));
+}
+
+// NEW op: fp16 paged write (PagedKVCache's fp16 mode), vLLM's reshape_and_cache.
+void reshape_and_cache(at::Tensor key, at::Tensor value, at::Tensor k_cache, at::Tensor v_cache,
+                       at::Tensor slot_mapping) {
+  check_write(key, value, k_cache, v_cache, nullptr, nullptr, slot_mapping, false);
+  const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
+  hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
+  check_status(pa_reshape_and_cache_f16(
+      key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
+      value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)key.size(0),
+      (int32_t)key.size(1), (int32_t)key.size(2), k_cache.data_ptr(), v_cache.data_ptr(),
+      (int32_t)k_cache.size(0), (int32_t)k_cache.size(3), (int32_t)k_cache.size(4),
       reinterpret_cast<pa_stream_t>(stream)));
 }
 
@@ -328,6 +382,9 @@ PYBIND11_MODULE(paged_attn_opt, m) {
   m.def("decode_plan", &decode_plan, "(partition_tokens, num_splits) the launcher would use");
   m.def("reshape_and_cache_int8", &reshape_and_cache_int8,
         "per-token INT8 quantize + paged cache write (new op)");
+  m.def("reshape_and_cache_int8_static", &reshape_and_cache_int8_static,
+        "INT8 quantize with one given scale per K / V tensor + paged cache write (new op)");
+  m.def("reshape_and_cache", &reshape_and_cache, "fp16 paged cache write (new op)");
   m.def("set_waves_per_group", [](int64_t w) { check_status(pa_decode_set_waves_per_group((int32_t)w)); },
         "tuning hook: force 4 or 8 waves per decode work-group (0 = automatic)");
   m.def("version", []() { return std::string(pa_version()); });

@@ -12,6 +12,9 @@ from .registry import (  # noqa: F401
     decode,
     decode_plan,
     paged_decode_attention,
+    reshape_and_cache,
     reshape_and_cache_int8,
+    reshape_and_cache_int8_static,
 )
+from .paged_cache import PagedKVCache  # noqa: F401
 from ._loader import capi, ext  # noqa: F401

@@ -35,6 +35,7 @@ HIP_SOURCES = [
     "pa_decode_d128.hip",
     "pa_decode_d256.hip",
     "pa_quant.hip",
+    "pa_cache_write.hip",
     "pa_probe.hip",
 ]
 HOST_SOURCES = ["pa_capi.cpp"]

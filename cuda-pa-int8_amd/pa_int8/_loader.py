@@ -73,6 +73,11 @@ PROTOTYPES = {
     "pa_paged_decode_attn_splitk_int8": (ctypes.c_int, _DECODE_I8_ARGS),
     "pa_reshape_and_cache_int8": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32,
                                                  _i32, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
+    "pa_reshape_and_cache_int8_static": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p,
+                                                        _i32, _i32, _i32, _p, _p, _p, _p, _p,
+                                                        _p, _i32, _i32, _i32, _p]),
+    "pa_reshape_and_cache_f16": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32,
+                                                _i32, _p, _p, _i32, _i32, _i32, _p]),
     "pa_probe_read_contiguous": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
     "pa_probe_read_chunks": (ctypes.c_int, [_p, _sz, _p, _i32, _i32, _p, _i32, _p]),
 }

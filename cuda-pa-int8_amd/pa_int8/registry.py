@@ -94,3 +94,18 @@ def reshape_and_cache_int8(key, value, k_cache, v_cache, k_scales, v_scales, slo
     """Quantize ``key/value [T, Hkv, D]`` fp16 per token and write them into the
     INT8 paged cache at ``slot_mapping`` (int64, ``block * block_size + off``)."""
     _ext().reshape_and_cache_int8(key, value, k_cache, v_cache, k_scales, v_scales, slot_mapping)
+
+
+def reshape_and_cache_int8_static(key, value, k_cache, v_cache, k_scales, v_scales, slot_mapping,
+                                  k_scale, v_scale):
+    """INT8 write with one fp32 scale for all of ``key`` and one for all of
+    ``value`` (1-element device tensors, read by the kernel): the per-tensor
+    mode of PagedKVCache (benchmarks/int8_bridge/paged_cache.py:99-106,140-142)."""
+    _ext().reshape_and_cache_int8_static(key, value, k_cache, v_cache, k_scales, v_scales,
+                                         slot_mapping, k_scale, v_scale)
+
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
+    """fp16 write of ``key/value [T, Hkv, D]`` into the paged fp16 cache at
+    ``slot_mapping`` (the fp16 mode of PagedKVCache, paged_cache.py:116-130,148-150)."""
+    _ext().reshape_and_cache(key, value, k_cache, v_cache, slot_mapping)

@@ -185,6 +185,37 @@ pa_status_t pa_reshape_and_cache_int8(
     void* k_cache, void* v_cache, float* k_scales, float* v_scales,
     int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
 
+/* Per-tensor INT8 quantize + paged-cache write.  NEW API (the reference
+ * quantizes with torch): the "int8_per_tensor" write path of PagedKVCache
+ * (benchmarks/int8_bridge/paged_cache.py:99-106 prefill, :140-142
+ * decode_append).  Every K element is quantized with *k_scale and every V
+ * element with *v_scale (one fp32 each, read on the device), as
+ * int8(clamp(rne(fp32(x) / scale), -127, 127)), and the scale is stored in
+ * each written slot of k_scales / v_scales.  Other arguments and rules as
+ * pa_reshape_and_cache_int8. */
+pa_status_t pa_reshape_and_cache_int8_static(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    void* k_cache, void* v_cache, float* k_scales, float* v_scales,
+    const float* k_scale, const float* v_scale,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
+
+/* FP16 paged-cache write (no quantization).  NEW API (the reference scatters
+ * with torch indexing): the "fp16" write path of PagedKVCache
+ * (benchmarks/int8_bridge/paged_cache.py:116-130 prefill, :148-150
+ * decode_append) and the placement of build_paged_kv_cache
+ * (tests/paged_decode_attn.py:85-99): k_cache[blk, h, :, off, :] =
+ * key[t, h].view(D/8, 8), v_cache[blk, h, :, off] = value[t, h], with
+ * slot_mapping[t] = blk * block_size + off.  block_size must be a multiple
+ * of 8 dividing 128; x must be 8; other rules as pa_reshape_and_cache_int8. */
+pa_status_t pa_reshape_and_cache_f16(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    void* k_cache, void* v_cache, int32_t num_blocks, int32_t block_size, int32_t x,
+    pa_stream_t stream);
+
 /* Measurement helpers (no reference counterpart): streaming-read probes that
  * give bench.py the practical HBM read rate next to the decode numbers.
  * pa_probe_read_contiguous sweeps `bytes` from `src` with 16-byte loads;

@@ -17,6 +17,11 @@ Yevsquant/cuda-PA-INT8) in vectorised numpy:
 * ``reshape_and_cache_int8``     placement of tests/paged_decode_attn.py:190-197
                                  and benchmarks/int8_bridge/paged_cache.py:132-156
                                  (slot = block * block_size + offset)
+* ``reshape_and_cache_int8_static``  the per-tensor write of
+                                 benchmarks/int8_bridge/paged_cache.py:99-106,140-142
+* ``reshape_and_cache_f16``      the fp16 write of paged_cache.py:116-130,148-150
+                                 (placement of tests/paged_decode_attn.py:85-99)
+* ``paged_cache_tensor_scale``   benchmarks/int8_bridge/paged_cache.py:101-102
 * ``dense_attention``            tests/test_paged_decode_attn.py:37-52
 
 How each one is pinned (checked against something other than itself) is
@@ -52,6 +57,9 @@ __all__ = [
     "build_paged_kv_cache_int8",
     "dequantize_kv",
     "reshape_and_cache_int8",
+    "reshape_and_cache_int8_static",
+    "reshape_and_cache_f16",
+    "paged_cache_tensor_scale",
     "gather_kv",
 ]
 
@@ -298,6 +306,24 @@ def dequantize_kv(k_cache, v_cache, k_scales, v_scales):
     return k, v
 
 
+def _place(slot_mapping, k_cache, v_cache, kq, vq, k_scales=None, v_scales=None, ks=None,
+           vs=None):
+    """Write per-token rows at their slots: K to ``k_cache[phys, h, :, off, :]``
+    as ``row.view(D/x, x)``, V to ``v_cache[phys, h, :, off]``, scales to
+    ``[phys, h, off]``; slots outside ``[0, NB * bs)`` are skipped."""
+    nb, hkv, dx, bs, x = k_cache.shape
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    ok = (slots >= 0) & (slots < nb * bs)
+    idx = np.nonzero(ok)[0]
+    phys = slots[idx] // bs
+    off = slots[idx] % bs
+    k_cache[phys, :, :, off, :] = kq[idx].reshape(len(idx), hkv, dx, x)
+    v_cache[phys, :, :, off] = vq[idx]
+    if k_scales is not None:
+        k_scales[phys, :, off] = ks[idx]
+        v_scales[phys, :, off] = vs[idx]
+
+
 def reshape_and_cache_int8(key, value, slot_mapping, k_cache, v_cache,
                            k_scales, v_scales):
     """Quantize ``key/value [T, Hkv, D]`` per token and write them in place.
@@ -317,12 +343,46 @@ def reshape_and_cache_int8(key, value, slot_mapping, k_cache, v_cache,
     assert hk == hkv and dx * x == d_
     kq, ks = quantize_per_token(key, axis=-1)
     vq, vs = quantize_per_token(value, axis=-1)
-    slots = np.asarray(slot_mapping, dtype=np.int64)
-    ok = (slots >= 0) & (slots < nb * bs)
-    idx = np.nonzero(ok)[0]
-    phys = slots[idx] // bs
-    off = slots[idx] % bs
-    k_cache[phys, :, :, off, :] = kq[idx].reshape(len(idx), hkv, dx, x)
-    v_cache[phys, :, :, off] = vq[idx]
-    k_scales[phys, :, off] = ks[idx]
-    v_scales[phys, :, off] = vs[idx]
+    _place(slot_mapping, k_cache, v_cache, kq, vq, k_scales, v_scales, ks, vs)
+
+
+def paged_cache_tensor_scale(x):
+    """Per-tensor scale of PagedKVCache.prefill (benchmarks/int8_bridge/paged_cache.py:101-102):
+    ``(x.abs().amax() / 127.0).to(float32).clamp_min(1e-8)``.
+
+    The division runs in x's dtype (fp16: one rounding to fp16), the clamp
+    after the conversion to float32, so ``amax = 0`` gives ``float32(1e-8)``
+    (``quantize_per_tensor`` clamps before dividing and gives 0 there).
+    """
+    x = np.asarray(x)
+    amax = np.abs(x).max()
+    if x.dtype == np.float16:
+        s = (np.float32(amax) / np.float32(127.0)).astype(np.float16).astype(np.float32)
+    else:
+        s = np.float32(np.float32(amax) / np.float32(127.0))
+    return np.float32(max(s, np.float32(1e-8)))
+
+
+def reshape_and_cache_int8_static(key, value, slot_mapping, k_cache, v_cache, k_scales,
+                                  v_scales, k_scale, v_scale):
+    """INT8 write with one given fp32 scale for all of K and one for V
+    (PagedKVCache "int8_per_tensor": ``_quantize_with_scale``,
+    benchmarks/int8_bridge/paged_cache.py:34-38,103-106,140-142); the scale is
+    stored in every written slot (``sk.expand``, :105-106)."""
+    key = np.asarray(key)
+    value = np.asarray(value)
+    t_ = key.shape[0]
+    kq = _quantize_with_scale(key, np.float32(k_scale))
+    vq = _quantize_with_scale(value, np.float32(v_scale))
+    hkv = key.shape[1]
+    ks = np.full((t_, hkv), np.float32(k_scale), np.float32)
+    vs = np.full((t_, hkv), np.float32(v_scale), np.float32)
+    _place(slot_mapping, k_cache, v_cache, kq, vq, k_scales, v_scales, ks, vs)
+
+
+def reshape_and_cache_f16(key, value, slot_mapping, k_cache, v_cache):
+    """fp16 write of ``key/value [T, Hkv, D]`` at their slots (PagedKVCache
+    "fp16", benchmarks/int8_bridge/paged_cache.py:116-130,148-150; the layout of
+    tests/paged_decode_attn.py:94-97)."""
+    _place(slot_mapping, k_cache, v_cache, np.asarray(key).astype(k_cache.dtype),
+           np.asarray(value).astype(v_cache.dtype))

@@ -210,3 +210,30 @@ def test_extension_exports_reference_op_names(built):
                "paged_decode_attn_splitk", "paged_decode_attn_warp_int8",
                "paged_decode_attn_splitk_int8", "paged_decode_attention"):
         assert callable(getattr(ext, op)), op
+
+
+def test_paged_cache_class_host_logic():
+    """PagedKVCache's shapes, identity table and byte accounting
+    (benchmarks/int8_bridge/paged_cache.py:41-86,158-182; the size gate of
+    tests/test_int8_bridge.py:98-108), constructed on the CPU: no kernel runs."""
+    import torch
+
+    import pa_int8
+
+    kw = dict(num_layers=28, num_kv_heads=2, head_dim=128, max_len=2048, block_size=16, x=8,
+              device="cpu")
+    fp16 = pa_int8.PagedKVCache(variant="fp16", **kw)
+    i8 = pa_int8.PagedKVCache(variant="int8_per_token", **kw)
+    assert fp16.k_cache.shape == (28, 128, 2, 16, 16, 8) and fp16.k_cache.dtype == torch.float16
+    assert i8.v_cache.shape == (28, 128, 2, 128, 16) and i8.v_cache.dtype == torch.int8
+    assert i8.k_scales.shape == (28, 128, 2, 16)
+    assert fp16.block_table.tolist() == [list(range(128))]
+    assert i8.kv_bytes() < fp16.kv_bytes() and i8.kv_bytes() / fp16.kv_bytes() < 0.6
+    assert fp16.kv_bytes_for_len(2048) == fp16.kv_bytes()
+    assert i8.kv_bytes_for_len(2048) == i8.kv_bytes()
+    assert i8.kv_bytes_for_len(17) == 2 * 28 * (2 * 2 * 128 * 16 + 2 * 2 * 16 * 4)
+    c = pa_int8.PagedKVCache(variant="int8_per_tensor", **kw)
+    assert c.context_lens(3).tolist() == [0] and c.lengths == [0] * 28
+    with pytest.raises(RuntimeError, match="CUDA"):
+        c.prefill(0, torch.zeros(5, 2, 128, dtype=torch.float16),
+                  torch.zeros(5, 2, 128, dtype=torch.float16))

@@ -292,3 +292,94 @@ def test_reshape_and_cache_matches_builder_placement():
     ref.reshape_and_cache_int8(k[:1, 0], v[:1, 0], np.array([ekc.shape[0] * 16]), ekc, evc, eks,
                                evs)
     assert np.array_equal(before, ekc)
+
+
+# ------------------------------------------- PagedKVCache write modes (oracle)
+
+def _float_rne(fr, mant_bits, emin):
+    """Exact rational -> nearest binary float with `mant_bits` fraction bits and
+    minimum normal exponent `emin` (ties to even), as a Fraction; no overflow."""
+    if fr == 0:
+        return Fraction(0)
+    sign = 1 if fr > 0 else -1
+    a = abs(fr)
+    e = math.floor(math.log2(a))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (max(e, emin) - mant_bits)
+    return sign * _rne_int(a / ulp) * ulp
+
+
+def test_paged_cache_tensor_scale_closed_form():
+    """(amax / 127) rounded in the input dtype, then widened, then clamped at
+    1e-8 (paged_cache.py:101-102), from exact rationals."""
+    amaxes = [0.0, 6e-8, 1e-6, 1.2e-5, 6.1e-5, 0.0077, 0.5, 1.0, 3.14159, 127.0, 1000.0, 65504.0]
+    for a in amaxes:
+        x = np.array([a, -a / 2, 0.0], np.float16)
+        a16 = Fraction(float(np.float16(a)))
+        s = _float_rne(a16 / 127, 10, -14)                 # fp16 division
+        want = max(float(s), float(np.float32(1e-8)))
+        got = ref.paged_cache_tensor_scale(x)
+        assert got.dtype == np.float32 and float(got) == float(np.float32(want)), a
+        y = np.array([a, -a / 3], np.float32)             # fp32 input: one fp32 rounding
+        s32 = _float_rne(Fraction(float(np.float32(a))) / 127, 23, -126)
+        want32 = max(float(s32), float(np.float32(1e-8)))
+        assert float(ref.paged_cache_tensor_scale(y)) == float(np.float32(want32)), a
+    # the clamp order differs from quantize_per_tensor at amax = 0
+    z = np.zeros(8, np.float16)
+    assert float(ref.paged_cache_tensor_scale(z)) == float(np.float32(1e-8))
+    assert float(ref.quantize_per_tensor(z)[1]) == 0.0
+
+
+def test_static_quant_matches_exact_rational_arithmetic():
+    """q = clamp(rne(fp32(x / s)), -127, 127) from exact rationals, including
+    saturation far beyond the scale, NaN -> 0 and inf -> +-127."""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(512) * 40).astype(np.float16)
+    x[:6] = [np.inf, -np.inf, np.nan, 0.0, 65504.0, -65504.0]
+    for s in (np.float32(1e-8), np.float32(0.0078125), np.float32(0.3), np.float32(2.7e-3)):
+        q = ref._quantize_with_scale(x, s)
+        for xi, qi in zip(x, q):
+            if np.isnan(xi):
+                want = 0
+            elif np.isinf(xi):
+                want = 127 if xi > 0 else -127
+            else:
+                quo = _float_rne(Fraction(float(xi)) / Fraction(float(s)), 23, -126)
+                want = max(-127, min(127, _rne_int(quo)))
+            assert int(qi) == want, (float(xi), float(s))
+
+
+def test_static_write_matches_per_tensor_builder():
+    """Writing with quantize_per_tensor's scales through slots equals the
+    per-tensor int8 builder (tests/paged_decode_attn.py:167-172,190-197)."""
+    rng = np.random.default_rng(6)
+    lens = np.array([40, 23], np.int32)
+    k = rng.standard_normal((2, 40, 2, 128)).astype(np.float16)
+    v = (rng.standard_normal((2, 40, 2, 128)) * 3).astype(np.float16)
+    kc, vc, ks, vs, bt = ref.build_paged_kv_cache_int8(k, v, lens, mode="per_tensor",
+                                                       rng=np.random.default_rng(2))
+    _, sk = ref.quantize_per_tensor(k)
+    _, sv = ref.quantize_per_tensor(v)
+    ekc, evc = np.zeros_like(kc), np.zeros_like(vc)
+    eks, evs = np.zeros_like(ks), np.zeros_like(vs)
+    seq = np.repeat(np.arange(2), lens)
+    tok = np.concatenate([np.arange(n) for n in lens])
+    slots = bt[seq, tok // 16].astype(np.int64) * 16 + tok % 16
+    ref.reshape_and_cache_int8_static(k[seq, tok], v[seq, tok], slots, ekc, evc, eks, evs, sk, sv)
+    assert np.array_equal(ekc, kc) and np.array_equal(evc, vc)
+    assert np.array_equal(eks, ks) and np.array_equal(evs, vs)
+
+
+def test_f16_write_matches_builder_placement():
+    c = fp16_case(3, make_lens(45, 3), 8, 2, seed=8)
+    kc = np.zeros_like(c["k_cache"])
+    vc = np.zeros_like(c["v_cache"])
+    lens, bt = c["lens"], c["block_table"]
+    seq = np.repeat(np.arange(3), lens)
+    tok = np.concatenate([np.arange(n) for n in lens])
+    slots = bt[seq, tok // 16].astype(np.int64) * 16 + tok % 16
+    ref.reshape_and_cache_f16(c["k"][seq, tok], c["v"][seq, tok], slots, kc, vc)
+    assert np.array_equal(kc, c["k_cache"]) and np.array_equal(vc, c["v_cache"])
