@@ -30,7 +30,7 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
                        int64_t kts, int64_t khs, int64_t vts, int64_t vhs,
                        const int64_t* __restrict__ slots, int num_tokens, int num_kv_heads,
                        half_t* __restrict__ kc, half_t* __restrict__ vc, int num_blocks, int bs,
-                       int njobs) {
+                       int bs_log2, int njobs) {
   constexpr int JQ = D / 32;   // 16-B groups per lane
   __shared__ __attribute__((aligned(16))) half_t tile[kWriteWaves][D * 16];
 
@@ -55,8 +55,9 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
     for (int j = 0; j < JQ; ++j) x[j] = *reinterpret_cast<const uint4*>(src + (qq + 4 * j) * 8);
     const int64_t slot = tv ? slots[tc] : -1;
     const bool sok = slot >= 0 && slot < pool;
-    const int64_t blk = sok ? slot / bs : 0;
-    const int off = sok ? (int)(slot - blk * bs) : 0;
+    // block_size is a power of two: shifts instead of a 64-bit division
+    const int64_t blk = sok ? (slot >> bs_log2) : 0;
+    const int off = sok ? (int)(slot & (bs - 1)) : 0;
     const int64_t bh = blk * num_kv_heads + h;
 
     if (!is_v) {
@@ -87,8 +88,8 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int64_t blk0 = slot0 / bs;
-      const int off0 = (int)(slot0 - blk0 * bs);
+      const int64_t blk0 = slot0 >> bs_log2;
+      const int off0 = (int)(slot0 & (bs - 1));
       const int64_t bh0 = blk0 * num_kv_heads + h;
       // Row rr of the tile (16 tokens of dim rr, 32 B) leaves as two 16-B halves.
 #pragma unroll
@@ -131,7 +132,7 @@ static hipError_t launch_write_d(const CacheWriteLaunch& l) {
       static_cast<const half_t*>(l.key), static_cast<const half_t*>(l.value), l.key_token_stride,
       l.key_head_stride, l.value_token_stride, l.value_head_stride, l.slot_mapping, l.num_tokens,
       l.num_kv_heads, static_cast<half_t*>(l.k_cache), static_cast<half_t*>(l.v_cache),
-      l.num_blocks, l.block_size, njobs);
+      l.num_blocks, l.block_size, __builtin_ctz((unsigned)l.block_size), njobs);
   return hipGetLastError();
 }
 

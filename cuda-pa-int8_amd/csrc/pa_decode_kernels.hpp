@@ -79,6 +79,17 @@ __device__ __forceinline__ float head_sum(float v) {
   return cross_half32(v, OpSum());
 }
 
+// Value of quad position b (lane 4k + b) in every lane of quad k.  b must
+// fold to a constant (unrolled loops).
+__device__ __forceinline__ float quad_bcast(float v, int b) {
+  switch (b) {
+    case 0: return dpp_mov<0x00>(v);
+    case 1: return dpp_mov<0x55>(v);
+    case 2: return dpp_mov<0xAA>(v);
+    default: return dpp_mov<0xFF>(v);
+  }
+}
+
 // 8 int8 values -> 8 fp16 values holding 1152 + value.
 __device__ __forceinline__ h8_t i8x8_biased(uint2 w) {
   uint32_t d[4];
@@ -217,26 +228,33 @@ struct SplitWork {
 // `after_issue` runs in every wave once the wave's first K/V loads are issued
 // (the scheduled kernel claims its next item there, so that no wait for this
 // split's data also waits for the claim).
-template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, typename AfterIssue>
+// `resolve(ctx, ns)` supplies the context length and split count once the
+// split's block-id loads are in flight (the grid kernel reads them from
+// memory then) and returns false when the split holds no tokens.
+template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, typename Resolve,
+          typename AfterIssue>
 __device__ __forceinline__ void decode_split(
     const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
     const float* __restrict__ ksc, const float* __restrict__ vsc, const int* __restrict__ bt,
     half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
-    uint32_t* __restrict__ cnt, const DecodeShape& sh, const SplitWork& wk,
-    DecodeSmem<D, NW>& sm, AfterIssue&& after_issue) {
+    uint32_t* __restrict__ cnt, const DecodeShape& sh, SplitWork wk,
+    DecodeSmem<D, NW>& sm, Resolve&& resolve, AfterIssue&& after_issue) {
   constexpr int KC = D / 32;                 // 32-dim k-chunks of one QK product
   constexpr int NT = D / 16;                 // 16-dim output tiles of PV
   constexpr int PAIRS = D <= 128 ? 2 : 1;    // 32-token pairs per wave iteration
   constexpr int IT = 32 * PAIRS;             // tokens per wave iteration
   constexpr int ESZ = I8 ? 1 : 2;            // bytes per cache element
   using LVec = typename std::conditional<I8, uint2, uint4>::type;   // 8 elements
+  // INT8 with head_dim <= 128 uses 16-byte loads throughout (W8): a K load
+  // holds one dim group of two adjacent tokens (t, t + 1), which feed the
+  // same row of the two QK MFMAs of a pair, and a V load holds 16 tokens of
+  // one dim, which feed both pairs.  Each lane loads the scales of 4 tokens
+  // and the others reach the lanes that need them by quad DPP broadcasts.
+  constexpr bool W8 = I8 && D <= 128;
 
   const int seq = wk.seq, kvh = wk.kvh, chunk = wk.chunk, split = wk.split;
   const int gt = sh.head_tile;
-  const int ns_eff = wk.ns;
   const int t_begin = split * wk.partition;
-  const int t_end = min(wk.ctx, t_begin + wk.partition);
-  const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
 
   // The thread index is made opaque here so that no lane-dependent address
   // math is hoisted out of a caller's loop over splits (it would stay live,
@@ -284,12 +302,29 @@ __device__ __forceinline__ void decode_split(
   int e_cur = I8 ? 0 : 14;
   const float c = sh.scale_log2;
 
-  // ---- the split's block ids, staged once in LDS.
+  // ---- the split's block ids, staged once in LDS.  Their loads cover every
+  // block the split can touch and are issued before the context length is
+  // known, so the two memory round trips overlap.
   const int b_first = t_begin >> bsl;
-  const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1,
-                                         split_blocks_max<NW>())
-                                   : 0;
-  for (int i = tid; i < nblk; i += NW * kWave) sm.blk[i] = btrow[b_first + i];
+  constexpr int kStageRegs = (split_blocks_max<NW>() + NW * kWave - 1) / (NW * kWave);
+  int nstage = min(((t_begin + wk.partition - 1) >> bsl) - b_first + 1, sh.max_blocks - b_first);
+  nstage = nstage < 0 ? 0 : min(nstage, split_blocks_max<NW>());
+  int staged[kStageRegs];
+#pragma unroll
+  for (int k = 0; k < kStageRegs; ++k) {
+    const int i = tid + k * NW * kWave;
+    staged[k] = i < nstage ? btrow[b_first + i] : 0;
+  }
+  if (!resolve(wk.ctx, wk.ns)) return;   // work-group uniform, before any barrier
+  const int ns_eff = wk.ns;
+  const int t_end = min(wk.ctx, t_begin + wk.partition);
+  const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
+  const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1, nstage) : 0;
+#pragma unroll
+  for (int k = 0; k < kStageRegs; ++k) {
+    const int i = tid + k * NW * kWave;
+    if (i < nstage) sm.blk[i] = staged[k];
+  }
   // LDS-only barrier: the writes above are complete (lgkmcnt 0) before it,
   // and no vector-memory wait is implied.
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -307,9 +342,26 @@ __device__ __forceinline__ void decode_split(
   LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
   float ksv[PAIRS][8], vsv[PAIRS][8];   // INT8 scales of this lane's 8 tokens
   int nvalid[PAIRS];                    // valid tokens among this lane's 8
+  // W8: K rows of tokens (t, t + 1); V rows of 16 tokens; scales of the 4
+  // tokens tok0 + 16g + 4(r & 3) + i, i = 0..3.
+  uint4 kw[PAIRS][KC], vw[NT];
+  float4 ks4, vs4;
+  bool sok4[4];                         // W8: those 4 tokens exist (masking)
 
   auto load_blocks = [&](int it_, Blocks& b) {
     const int tok0 = t_begin + it_ * IT;
+    if constexpr (W8) {
+      // K rows of lane (r, g) lie in the 16-token group tok0 + 16(r >> 2), its V
+      // rows and scales in tok0 + 16g; a group never straddles a block
+      // (block_size is a multiple of 16).
+      const int kg = tok0 + 16 * (r >> 2);
+      const int tg = tok0 + 16 * g;
+      const int ki = ((kg < t_end ? kg : t_begin) >> bsl) - b_first;
+      const int vi = ((tg < t_end ? tg : t_begin) >> bsl) - b_first;
+      b.kb[0] = sm.blk[ki < nblk ? ki : 0];
+      b.vb[0] = sm.blk[vi < nblk ? vi : 0];
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
       const int kg = tok0 + 32 * p + 8 * (r >> 2);
@@ -323,6 +375,20 @@ __device__ __forceinline__ void decode_split(
   // K rows: token tok0 + 32p + 8(r>>2) + (r&3) (first MFMA) and + 4 (second).
   auto issue_k = [&](int it_, const Blocks& b) {
     const int tok0 = t_begin + it_ * IT;
+    if constexpr (W8) {
+      // Row r of pair p: tokens tok0 + 16(r >> 2) + 8p + 2(r & 3) and + 1.
+      const int kg = tok0 + 16 * (r >> 2);
+      const int kgc = kg < t_end ? kg : t_begin;
+      const int kb = (unsigned)b.kb[0] < (unsigned)sh.num_blocks ? b.kb[0] : 0;
+      const uint8_t* kp = kc + ((((size_t)kb * hkv + kvh) * (D / 8) + g) * bs +
+                                (kgc & (bs - 1)) + 2 * (r & 3)) * 8;
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk)
+          kw[p][kk] = *reinterpret_cast<const uint4*>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
       const int kg = tok0 + 32 * p + 8 * (r >> 2);
@@ -341,6 +407,28 @@ __device__ __forceinline__ void decode_split(
   // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7.
   auto issue_v = [&](int it_, const Blocks& b) {
     const int tok0 = t_begin + it_ * IT;
+    if constexpr (W8) {
+      // V rows: dim 16t + r, tokens tok0 + 16g .. + 15 (pair p uses 8p .. 8p + 7).
+      const int tg = tok0 + 16 * g;
+      const int tgc = tg < t_end ? tg : t_begin;
+      const bool vok = (unsigned)b.vb[0] < (unsigned)sh.num_blocks;
+      const int vb = vok ? b.vb[0] : 0;
+      const int voff = tgc & (bs - 1);
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+        const int t0 = tg + 8 * p;
+        nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sok4[i] = vok && tg + 4 * (r & 3) + i < t_end;
+      const uint8_t* vp = vc + (((size_t)vb * hkv + kvh) * D + r) * bs + voff;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) vw[t] = *reinterpret_cast<const uint4*>(vp + (size_t)(16 * t) * bs);
+      const size_t slot = ((size_t)vb * hkv + kvh) * bs + voff + 4 * (r & 3);
+      ks4 = *reinterpret_cast<const float4*>(ksc + slot);
+      vs4 = *reinterpret_cast<const float4*>(vsc + slot);
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
       const int tg = tok0 + 32 * p + 8 * g;
@@ -376,22 +464,41 @@ __device__ __forceinline__ void decode_split(
     auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask) {
       // ---- online softmax (lane-local except the per-head max)
       float mloc = kNegInf;
+      // W8: this lane's 4 scales; token 16g + 8p + j of the lane's row is held
+      // by quad position 2p + (j >> 2), element j & 3.
+      float ksa[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+      float vsa[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+      if constexpr (W8) {
+        if (need_mask) {
 #pragma unroll
-      for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float v;
-          if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
-          else v = s[p][j] * c;
-          s[p][j] = v;
+          for (int i = 0; i < 4; ++i) vsa[i] = sok4[i] ? vsa[i] : 0.f;
         }
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float ksj = quad_bcast(ksa[j & 3], 2 * p + (j >> 2));
+            vsv[p][j] = quad_bcast(vsa[j & 3], 2 * p + (j >> 2));
+            s[p][j] = (s[p][j] - qbias) * (ksj * c);
+          }
+      } else {
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float v;
+            if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
+            else v = s[p][j] * c;
+            s[p][j] = v;
+          }
+      }
       if (need_mask) {
 #pragma unroll
         for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             s[p][j] = j < nvalid[p] ? s[p][j] : kNegInf;
-            if constexpr (I8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
+            if constexpr (I8 && !W8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
           }
       }
 #pragma unroll
@@ -406,10 +513,17 @@ __device__ __forceinline__ void decode_split(
       float wsc;
       if constexpr (I8) {
         float msv = 0.f;
+        if constexpr (W8) {
+          // The 64 tokens' scales are spread over the quads of a row and the 4 rows.
+          msv = fmaxf(fmaxf(vsa[0], vsa[1]), fmaxf(vsa[2], vsa[3]));
+          msv = fmaxf(msv, dpp_mov<kQuadXor1>(msv));
+          msv = fmaxf(msv, dpp_mov<kQuadXor2>(msv));
+        } else {
 #pragma unroll
-        for (int p = 0; p < PAIRS; ++p)
+          for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
+            for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
+        }
         // Every head's lanes see the same tokens, so this max is wave-uniform.
         msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
         // Keep the weight exponent while the largest weight stays in [2^12, 2^15).
@@ -450,7 +564,9 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           h8_t av;
-          if constexpr (I8) {
+          if constexpr (W8) {
+            av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y) : make_uint2(vw[t].z, vw[t].w));
+          } else if constexpr (I8) {
             av = i8x8_exact(vr[p][t]);
           } else {
             uint4 v = vr[p][t];
@@ -462,14 +578,17 @@ __device__ __forceinline__ void decode_split(
       }
     };
     auto qk = [&](float (&s)[PAIRS][8]) {
-      // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r
+      // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r (W8: tok0 + 16g + 8p + j)
 #pragma unroll
       for (int p = 0; p < PAIRS; ++p) {
         f4_t sx = {0.f, 0.f, 0.f, 0.f}, sy = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk) {
           h8_t ax, ay;
-          if constexpr (I8) {
+          if constexpr (W8) {
+            ax = i8x8_biased(make_uint2(kw[p][kk].x, kw[p][kk].y));   // token T
+            ay = i8x8_biased(make_uint2(kw[p][kk].z, kw[p][kk].w));   // token T + 1
+          } else if constexpr (I8) {
             ax = i8x8_biased(kx[p][kk]);
             ay = i8x8_biased(ky[p][kk]);
           } else {
@@ -481,8 +600,14 @@ __device__ __forceinline__ void decode_split(
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          s[p][e] = sx[e];
-          s[p][4 + e] = sy[e];
+          if constexpr (W8) {
+            // rows 4g + e: tokens tok0 + 16g + 8p + 2e (sx) and + 1 (sy)
+            s[p][2 * e] = sx[e];
+            s[p][2 * e + 1] = sy[e];
+          } else {
+            s[p][e] = sx[e];
+            s[p][4 + e] = sy[e];
+          }
         }
       }
     };
@@ -633,16 +758,18 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
 
   // Contexts are clamped to what the block table holds and to what the grid's
   // splits cover, so no work-group reads past the table or the partials.
-  const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
-  int ctx = ctxl[seq];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
-  if (split >= ns_eff) return;
+  // The length is used only after the split's block-id loads are issued.
+  const int ctx_raw = ctxl[seq];
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
-  const SplitWork wk{seq, kvh, chunk, split, ctx, sh.partition, ns_eff,
-                     (size_t)unit * sh.nsplit, 1};
+  const SplitWork wk{seq, kvh, chunk, split, 0, sh.partition, 0, (size_t)unit * sh.nsplit, 1};
+  auto resolve = [&](int& ctx, int& ns) {
+    const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
+    ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
+    ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
+    return split < ns;
+  };
   decode_split<D, NW, I8, FUSED, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk, sm,
-                                        [] {});
+                                        resolve, [] {});
 }
 
 // ---------------------------------------------------------------------------
@@ -897,7 +1024,7 @@ decode_sched_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
     decode_split<D, NW, I8, FUSED, true>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
-                                         sm, claim);
+                                         sm, [](int&, int&) { return true; }, claim);
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
     // the last one and resets the counter for the next launch.

@@ -142,7 +142,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
                    int64_t khs, int64_t vts, int64_t vhs, const int64_t* __restrict__ slots,
                    int num_tokens, int num_kv_heads, int8_t* __restrict__ kc,
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
-                   int num_blocks, int bs, int njobs, const float* __restrict__ k_scale_in,
+                   int num_blocks, int bs, int bs_log2, int njobs, const float* __restrict__ k_scale_in,
                    const float* __restrict__ v_scale_in) {
   constexpr int JQ = QuantJob<D>::JQ;
   __shared__ __attribute__((aligned(16))) uint8_t tile[kQuantWaves][D * 16];
@@ -222,8 +222,9 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     }
     const float r = 1.0f / s;                           // IEEE reciprocal (inf when s = 0)
 
-    const int64_t blk = sok ? slot / bs : 0;
-    const int off = sok ? (int)(slot - blk * bs) : 0;
+    // block_size is a power of two: shifts instead of a 64-bit division
+    const int64_t blk = sok ? (slot >> bs_log2) : 0;
+    const int off = sok ? (int)(slot & (bs - 1)) : 0;
     const int64_t bh = blk * num_kv_heads + h;   // (block, kv_head) row
 
     // V: 16 tokens filling one aligned 16-slot run of a block are transposed
@@ -261,8 +262,8 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int64_t blk0 = slot0 / bs;
-      const int off0 = (int)(slot0 - blk0 * bs);
+      const int64_t blk0 = slot0 >> bs_log2;
+      const int off0 = (int)(slot0 & (bs - 1));
       const int64_t bh0 = blk0 * num_kv_heads + h;
 #pragma unroll
       for (int rr = lane; rr < D; rr += kWave) {
@@ -325,7 +326,8 @@ static hipError_t launch_quant_d(const QuantLaunch& l) {
       static_cast<const half_t*>(l.key), static_cast<const half_t*>(l.value), l.key_token_stride,
       l.key_head_stride, l.value_token_stride, l.value_head_stride, l.slot_mapping, l.num_tokens,
       l.num_kv_heads, static_cast<int8_t*>(l.k_cache), static_cast<int8_t*>(l.v_cache),
-      l.k_scales, l.v_scales, l.num_blocks, l.block_size, njobs, l.k_scale_in, l.v_scale_in);
+      l.k_scales, l.v_scales, l.num_blocks, l.block_size, __builtin_ctz((unsigned)l.block_size),
+      njobs, l.k_scale_in, l.v_scale_in);
   return hipGetLastError();
 }
 
