@@ -270,6 +270,26 @@ __device__ __forceinline__ void decode_split(
   const int bs = sh.block_size, bsl = sh.bs_log2;
   const int hkv = sh.num_kv_heads;
 
+  float m_run = kNegInf, l_part = 0.f;
+  f4_t acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+  int e_cur = I8 ? 0 : 14;
+  const float c = sh.scale_log2;
+
+  // ---- the split's block ids, staged once in LDS.  Their loads cover every
+  // block the split can touch and are issued before the context length is
+  // known, so the two memory round trips overlap.
+  const int b_first = t_begin >> bsl;
+  constexpr int kStageRegs = (split_blocks_max<NW>() + NW * kWave - 1) / (NW * kWave);
+  int nstage = min(((t_begin + wk.partition - 1) >> bsl) - b_first + 1, sh.max_blocks - b_first);
+  nstage = nstage < 0 ? 0 : min(nstage, split_blocks_max<NW>());
+  int staged[kStageRegs];
+#pragma unroll
+  for (int k = 0; k < kStageRegs; ++k) {
+    const int i = tid + k * NW * kWave;
+    staged[k] = i < nstage ? btrow[b_first + i] : 0;
+  }
   // ---- query operand: lane (r, g) holds q[head r][32kk + 8g .. +7]
   h8_t qreg[KC];
   {
@@ -295,26 +315,6 @@ __device__ __forceinline__ void decode_split(
     qbias = 1152.f * head_sum(s);
   }
 
-  float m_run = kNegInf, l_part = 0.f;
-  f4_t acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
-  int e_cur = I8 ? 0 : 14;
-  const float c = sh.scale_log2;
-
-  // ---- the split's block ids, staged once in LDS.  Their loads cover every
-  // block the split can touch and are issued before the context length is
-  // known, so the two memory round trips overlap.
-  const int b_first = t_begin >> bsl;
-  constexpr int kStageRegs = (split_blocks_max<NW>() + NW * kWave - 1) / (NW * kWave);
-  int nstage = min(((t_begin + wk.partition - 1) >> bsl) - b_first + 1, sh.max_blocks - b_first);
-  nstage = nstage < 0 ? 0 : min(nstage, split_blocks_max<NW>());
-  int staged[kStageRegs];
-#pragma unroll
-  for (int k = 0; k < kStageRegs; ++k) {
-    const int i = tid + k * NW * kWave;
-    staged[k] = i < nstage ? btrow[b_first + i] : 0;
-  }
   if (!resolve(wk.ctx, wk.ns)) return;   // work-group uniform, before any barrier
   const int ns_eff = wk.ns;
   const int t_end = min(wk.ctx, t_begin + wk.partition);
@@ -732,14 +732,37 @@ __device__ __forceinline__ void decode_split(
   }
 }
 
+// The first ten DecodeShape fields as plain int kernel arguments (after the
+// block-table and context-length pointers): aggregates are not preloaded into
+// SGPRs, scalars are.  The kernels rebuild the shape from them.
+#define PA_SHAPE_HEAD_PARAMS                                                              \
+  int sh_nchunk, int sh_num_items, int sh_nsplit, int sh_num_kv_heads, int sh_partition, \
+      int sh_max_blocks, int sh_bs_log2, int sh_block_size, int sh_num_seqs, int sh_num_blocks
+#define PA_SHAPE_HEAD_ARGS(s)                                                             \
+  (s).nchunk, (s).num_items, (s).nsplit, (s).num_kv_heads, (s).partition, (s).max_blocks, \
+      (s).bs_log2, (s).block_size, (s).num_seqs, (s).num_blocks
+#define PA_SHAPE_REBUILD(sh, tail)                                                        \
+  DecodeShape sh = tail;                                                                  \
+  sh.nchunk = sh_nchunk;                                                                  \
+  sh.num_items = sh_num_items;                                                            \
+  sh.nsplit = sh_nsplit;                                                                  \
+  sh.num_kv_heads = sh_num_kv_heads;                                                      \
+  sh.partition = sh_partition;                                                            \
+  sh.max_blocks = sh_max_blocks;                                                          \
+  sh.bs_log2 = sh_bs_log2;                                                                \
+  sh.block_size = sh_block_size;                                                          \
+  sh.num_seqs = sh_num_seqs;                                                              \
+  sh.num_blocks = sh_num_blocks
+
 // Grid form: one work-group per (unit, split) slot of the host's plan.
 template <int D, int NW, bool I8, bool FUSED>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
-decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
+decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE_HEAD_PARAMS,
+              DecodeShape sh_tail, const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
               const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
-              const float* __restrict__ vsc, const int* __restrict__ bt,
-              const int* __restrict__ ctxl, half_t* __restrict__ out, float* __restrict__ pacc,
-              float* __restrict__ pml, uint32_t* __restrict__ cnt, DecodeShape sh) {
+              const float* __restrict__ vsc, half_t* __restrict__ out, float* __restrict__ pacc,
+              float* __restrict__ pml, uint32_t* __restrict__ cnt) {
+  PA_SHAPE_REBUILD(sh, sh_tail);
   static_assert(sizeof(DecodeSmem<D, NW>) * (kWavesPerCU / NW) <= kLdsPerCU, "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
 
@@ -758,11 +781,16 @@ decode_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
 
   // Contexts are clamped to what the block table holds and to what the grid's
   // splits cover, so no work-group reads past the table or the partials.
-  // The length is used only after the split's block-id loads are issued.
-  const int ctx_raw = ctxl[seq];
+  // The length is used only after the split's block-id loads are issued.  It
+  // is read with a vector load at the top: a scalar load would be scheduled
+  // next to its first use, after the argument fetches of the query pointer.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const int ctx_lane = ctxl[seq + zero];
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
   const SplitWork wk{seq, kvh, chunk, split, 0, sh.partition, 0, (size_t)unit * sh.nsplit, 1};
   auto resolve = [&](int& ctx, int& ns) {
+    const int ctx_raw = __builtin_amdgcn_readfirstlane(ctx_lane);
     const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
     ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
@@ -965,12 +993,13 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
 
 template <int D, int NW, bool I8, bool FUSED>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
-decode_sched_kernel(const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
-                    const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
-                    const float* __restrict__ vsc, const int* __restrict__ bt,
-                    const int* __restrict__ ctxl, half_t* __restrict__ out,
-                    float* __restrict__ pacc, float* __restrict__ pml, uint32_t* __restrict__ cnt,
-                    DecodeShape sh, SchedArgs sa) {
+decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
+                    PA_SHAPE_HEAD_PARAMS, DecodeShape sh_tail, const half_t* __restrict__ q,
+                    const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
+                    const float* __restrict__ ksc, const float* __restrict__ vsc,
+                    half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
+                    uint32_t* __restrict__ cnt, SchedArgs sa) {
+  PA_SHAPE_REBUILD(sh, sh_tail);
   static_assert((sizeof(DecodeSmem<D, NW>) + sizeof(SchedSmem)) * (kWavesPerCU / NW) <= kLdsPerCU,
                 "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
@@ -1101,13 +1130,13 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
     auto* out = static_cast<half_t*>(l.out);
     if (l.fused) {
       decode_sched_kernel<D, NW, I8, true><<<l.groups, NW * kWave, 0, l.stream>>>(
-          q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
-          l.part_ml, l.counters, sh, sa);
+          l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+          l.part_ml, l.counters, sa);
       return hipGetLastError();
     }
     decode_sched_kernel<D, NW, I8, false><<<l.groups, NW * kWave, 0, l.stream>>>(
-        q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
-        l.part_ml, l.counters, sh, sa);
+        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+        l.part_ml, l.counters, sa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
@@ -1122,13 +1151,13 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
   auto* out = static_cast<half_t*>(l.out);
   if (l.fused) {
     decode_kernel<D, NW, I8, true><<<grid, NW * kWave, 0, l.stream>>>(
-        q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc,
-        l.part_ml, l.counters, sh);
+        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+        l.part_ml, l.counters);
     return hipGetLastError();
   }
   decode_kernel<D, NW, I8, false><<<grid, NW * kWave, 0, l.stream>>>(
-      q, kc, vc, l.k_scales, l.v_scales, l.block_table, l.context_lens, out, l.part_acc, l.part_ml,
-      l.counters, sh);
+      l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+      l.part_ml, l.counters);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;

@@ -22,20 +22,25 @@ constexpr int kSchedItemsPerGroup = 4;
 constexpr int kSchedQueueStride = 32;   // words between the 8 claim counters (128 B)
 
 // Shape of one decode launch, shared by every decode kernel.
+// The decode kernels take (block_table, context_lens, DecodeShape, ...) as
+// their first arguments and the library is built to preload the first 14
+// argument dwords into SGPRs: the two pointers and the first ten fields
+// below, which is all a work-group needs to find its work item and issue its
+// block-id and context-length loads without first fetching its arguments.
 struct DecodeShape {
-  int num_seqs;
-  int num_heads;
+  int nchunk;       // group / head_tile
+  int num_items;    // num_seqs * num_kv_heads * nsplit
+  int nsplit;       // splits present in the grid
   int num_kv_heads;
+  int partition;    // tokens per split, multiple of kIterTokens
+  int max_blocks;   // block_table row stride
+  int bs_log2;
+  int block_size;
+  int num_seqs;
+  int num_blocks;
+  int num_heads;
   int group;        // num_heads / num_kv_heads
   int head_tile;    // query heads per work-group (<= kMaxGroupTile)
-  int nchunk;       // group / head_tile
-  int block_size;
-  int bs_log2;
-  int num_blocks;
-  int max_blocks;   // block_table row stride
-  int partition;    // tokens per split, multiple of kIterTokens
-  int nsplit;       // splits present in the grid
-  int num_items;    // num_seqs * num_kv_heads * nsplit
   float scale_log2; // softmax scale * log2(e)
 };
 

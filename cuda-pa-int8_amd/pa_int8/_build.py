@@ -48,6 +48,10 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     # Keep the compiler from forming packed fp32 ops (v_pk_fma_f32 & co.).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Preload the first 14 kernel-argument dwords into SGPRs (the decode
+    # kernels put what their prologue needs there); the compiler adds the
+    # fallback that loads them itself under firmware that does not preload.
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Wno-unused-command-line-argument",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
