@@ -41,12 +41,19 @@ constexpr int kQuantWaves = 4;
 
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
-// |fl(x * fl(1/s)) - fl(x / s)| <= 127.5 * 2^-23 + 2^-18 < 1.9e-5 whenever
-// |x / s| < 128 (two roundings of the product, half an ulp of the quotient).
-// A product farther than this from every half-integer therefore rounds to the
-// same integer as the IEEE quotient the reference computes.
-constexpr float kTieGuard = 3.0e-5f;
+// The fast path multiplies by r, the hardware reciprocal of s (within 1 ulp
+// of 1/s), instead of dividing.  With |x / s| < 128:
+//   |fl(x * r) - x / s| <= 128 * (2^-23 + 2^-24) ~ 2.3e-5   (r, then the product)
+//   |fl(x / s) - x / s| <= 2^-18 ~ 3.8e-6                    (the reference's quotient)
+// so a product farther than 2.7e-5 from every half-integer rounds to the same
+// integer as the IEEE quotient the reference computes.  The guard keeps a margin.
+constexpr float kTieGuard = 4.0e-5f;
 constexpr float kRoundMagic = 12582912.0f;   // 1.5 * 2^23: y + magic rounds y to an integer (RNE)
+// fp16(a / 127) == fp16(fl(a * fl(1/127))) for every fp16 value a and for the
+// clamp value 1e-8: a / 127 is never an fp16 rounding midpoint and stays more
+// than 2^-18 (relative) away from one, beyond the 2^-23 error of the product
+// (checked exhaustively on the CPU).
+constexpr float kInv127 = 1.0f / 127.0f;
 
 // Exact path: rne(x / s) with IEEE division, clamped to [-127, 127], NaN -> 0.
 __device__ __forceinline__ uint32_t quant_exact_byte(float x, float s) {
@@ -57,13 +64,16 @@ __device__ __forceinline__ uint32_t quant_exact_byte(float x, float s) {
 
 // Quantizes the 8 fp16 values of one 16-B group to 8 bytes with the
 // reciprocal.  `slow` is set when some element's product lies within
-// kTieGuard of a half-integer (or is not finite): the fast byte is then not
-// provably the reference's and the caller redoes the group exactly.  With a
-// normal fp16 scale, |x / s| <= 127 * (1 + 2^-11) < 127.5 for every element of
-// the row, so no range check is needed here.
+// kTieGuard of a half-integer: the fast byte is then not provably the
+// reference's and the caller redoes the group exactly.  With a normal fp16
+// scale, |x / s| <= 127 * (1 + 2^-11) < 127.5 for every element of the row, so
+// no range check is needed, and the inputs are finite (a NaN or inf in the row
+// makes the scale non-normal, which takes the exact path): the largest
+// distance to an integer over the group decides with one comparison.
 __device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow) {
   const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t bytes[8];
+  float dmax = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
@@ -71,10 +81,11 @@ __device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow)
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const float y = xs[e] * r;
-      slow = slow || !(__builtin_fabsf(y - __builtin_rintf(y)) < 0.5f - kTieGuard);
+      dmax = fmaxf(dmax, __builtin_fabsf(y - __builtin_rintf(y)));
       bytes[2 * k + e] = __builtin_bit_cast(uint32_t, y + kRoundMagic);   // low byte = rne(y) mod 256
     }
   }
+  slow = slow || !(dmax < 0.5f - kTieGuard);
   uint2 out;
   out.x = __builtin_amdgcn_perm(__builtin_amdgcn_perm(bytes[3], bytes[2], 0x0c0c0400u),
                                 __builtin_amdgcn_perm(bytes[1], bytes[0], 0x0c0c0400u), 0x05040100u);
@@ -126,6 +137,24 @@ __device__ __forceinline__ uint2 quant_group_exact(uint4 xv, float s) {
                     b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
 }
 
+// Cache policy of the cache-tile stores (buffer store aux bits): sc1, the
+// write-through policy.  With the inputs read non-temporally it took the
+// config-3 write (524,288 tokens x 2 heads) from 169 to 156 us on MI355X: the
+// written tiles leave the L2 at once instead of as later write-backs between
+// the input reads.
+constexpr int kTileStorePolicy = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+
+// Inputs are read once: non-temporal loads keep them from displacing the L2.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+  const u4v_t t = __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+
 // The 16-B input groups of one job for one lane, and the lane's token slot.
 template <int D>
 struct QuantJob {
@@ -168,7 +197,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     const half_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
                              : key + (int64_t)tc * kts + (int64_t)h * khs;
 #pragma unroll
-    for (int j = 0; j < JQ; ++j) J.x[j] = *reinterpret_cast<const uint4*>(src + (qq + 4 * j) * 8);
+    for (int j = 0; j < JQ; ++j) J.x[j] = load_stream16(src + (qq + 4 * j) * 8);
   };
 
   // Two jobs stay in flight ahead of the one being quantized.  A prefetch
@@ -215,25 +244,35 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       am = rows_umax(am);
       const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
       const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
-      s = (float)(half_t)(a / 127.0f);                    // fp16 division, RNE
+      s = (float)(half_t)(a * kInv127);                   // == fp16(a / 127), RNE
       // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
       // sends the token's elements to the exact path.
       s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
     }
-    const float r = 1.0f / s;                           // IEEE reciprocal (inf when s = 0)
+    // Per-token scales are normal fp16 numbers on the fast path, so the
+    // hardware reciprocal is finite and within the guard's error budget; a
+    // caller's scale (per-tensor mode) takes the IEEE reciprocal.
+    const float r = STATIC ? 1.0f / s : __builtin_amdgcn_rcpf(s);
 
     // block_size is a power of two: shifts instead of a 64-bit division
     const int64_t blk = sok ? (slot >> bs_log2) : 0;
     const int off = sok ? (int)(slot & (bs - 1)) : 0;
     const int64_t bh = blk * num_kv_heads + h;   // (block, kv_head) row
 
-    // V: 16 tokens filling one aligned 16-slot run of a block are transposed
-    // through LDS and leave as 16-B rows.
+    // 16 tokens filling one aligned 16-slot run of a block (prefill): K rows
+    // and V rows then lie in one (block, kv head) tile each, stored through a
+    // buffer resource over that tile; V is transposed through LDS and leaves
+    // as 16-B rows.
     const int64_t slot0 = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(slot & 0xFFFFFFFF)) |
                           ((int64_t)__builtin_amdgcn_readfirstlane((int)(slot >> 32)) << 32);
     const bool mine = tv && slot == slot0 + i;
-    const bool vfast = is_v && (t0 + 16 <= num_tokens) && slot0 >= 0 && (slot0 & 15) == 0 &&
+    const bool run16 = (t0 + 16 <= num_tokens) && slot0 >= 0 && (slot0 & 15) == 0 &&
                        slot0 + 16 <= pool && __builtin_amdgcn_ballot_w64(!mine) == 0;
+    const bool vfast = is_v && run16;
+    const int64_t bh0 = (slot0 >> bs_log2) * num_kv_heads + h;   // the run's tile (run16)
+    const int off0 = (int)(slot0 & (bs - 1));
+    const uint32_t tile_bytes = (uint32_t)(D * bs);
+    const auto ktile = tile_rsrc(kc + bh0 * D * bs, tile_bytes);
 
     // One 16-B group at a time: quantize, fix rare elements exactly, store.
 #pragma unroll
@@ -246,7 +285,13 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       }
       const int o = qq + 4 * j;   // dim group: dims 8o .. 8o+7
       if (!is_v) {
-        if (sok) *reinterpret_cast<uint2*>(kc + ((bh * (D / 8) + o) * bs + off) * 8) = qj;
+        if (run16) {
+          typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
+          __builtin_amdgcn_raw_buffer_store_b64((u2v_t){qj.x, qj.y}, ktile, (o * bs + off) * 8, 0,
+                                                kTileStorePolicy);
+        } else if (sok) {
+          *reinterpret_cast<uint2*>(kc + ((bh * (D / 8) + o) * bs + off) * 8) = qj;
+        }
       } else if (vfast) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -262,13 +307,12 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int64_t blk0 = slot0 >> bs_log2;
-      const int off0 = (int)(slot0 & (bs - 1));
-      const int64_t bh0 = blk0 * num_kv_heads + h;
+      const auto vtile = tile_rsrc(vc + bh0 * D * bs, tile_bytes);
 #pragma unroll
       for (int rr = lane; rr < D; rr += kWave) {
-        const uint4 row = *reinterpret_cast<const uint4*>(&tile[w][rr * 16]);
-        *reinterpret_cast<uint4*>(vc + (bh0 * D + rr) * bs + off0) = row;
+        typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+        const u4v_t row = *reinterpret_cast<const u4v_t*>(&tile[w][rr * 16]);
+        __builtin_amdgcn_raw_buffer_store_b128(row, vtile, rr * bs + off0, 0, kTileStorePolicy);
       }
       // The tile is rewritten by this wave's next job only after every lane
       // has read its rows.
