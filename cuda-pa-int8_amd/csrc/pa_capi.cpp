@@ -24,6 +24,8 @@ constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
 constexpr int kSchedMinPartition = 1024;   // per 4 waves, in-kernel schedule
 std::atomic<int> g_waves_override{0};
 std::atomic<int> g_schedule_mode{0};   // 0 auto, 1 grid, 2 in-kernel schedule
+std::atomic<int> g_load_mode{0};       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
+constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
 // Upper bound on resident decode work-groups used to size the partial
 // buffers of the in-kernel schedule (256 CUs x 2 groups on MI355X).
 constexpr int kSchedGroupsBound = 1024;
@@ -58,6 +60,8 @@ struct Plan {
   bool sched = false;
   int rows_max = 0;
   int pmin = 0, pmax = 0;
+  int pmin_uniform = 0;   // lower bound the kernel uses when all lengths are equal
+  bool nt_loads = false;  // non-temporal cache-tile loads
 };
 
 Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_heads,
@@ -92,6 +96,20 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   p.partition = (int)part;
   p.nsplit = (int)((ctx + part - 1) / part);
 
+  // Cache-tile loads: non-temporal when every K/V byte is read by exactly one
+  // work-group (one head chunk per kv head); MI355X streams them faster (FP16
+  // config 3: 94 -> 84 us, config 4 32k: 184 -> 166 us).  With several head
+  // chunks per kv head the chunks find the tiles in the L2 only with plain
+  // loads (MQA 32/1 of config 5: 71 us plain, 95 us non-temporal).
+  // A launch that reads little (bound: every sequence at `ctx` tokens) is
+  // latency-bound and its tiles may still sit in the 256 MB Infinity Cache
+  // from an earlier call, which plain loads can hit (config 1: 4.6 us plain,
+  // 6.0 us non-temporal); non-temporal loads start at 32 MB.
+  const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
+                             (is_f16(kind) ? 2 : 1);
+  const int lm = g_load_mode.load(std::memory_order_relaxed);
+  p.nt_loads = lm == 2 || (lm == 0 && p.nchunk == 1 && kv_bytes > kNtMinBytes);
+
   // Work distribution.  The split-K kinds (long and ragged contexts) use the
   // in-kernel schedule: no empty work-groups and largest-first items (config
   // 5 of the bench: 10-37% faster than the grid).  The single-launch kinds
@@ -101,11 +119,14 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   if (num_seqs > pa::kSchedMaxSeqs) p.sched = false;
   if (p.sched) {
     if (partition_tokens > 0) {
-      p.pmin = p.pmax = p.partition;
+      p.pmin = p.pmax = p.pmin_uniform = p.partition;
     } else {
       // Items below ~1 MB of FP16 K/V pay their fixed start-up and merge
       // costs too often (partition sweeps of the ragged mix on MI355X).
       p.pmin = kSchedMinPartition * p.waves / 4;
+      // Equal lengths: one item per resident work-group, down to the grid
+      // plan's bound (config 2 would otherwise run on half the work-groups).
+      p.pmin_uniform = kMinPartition * p.waves / 4;
       p.pmax = (int)hi;
     }
     // rows <= S + ceil(T / P), and the kernel keeps T / P <= max(groups * K / Hkv,
@@ -180,6 +201,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.sched = p.sched;
   l.rows_max = p.rows_max;
   l.pmin = p.pmin;
+  l.pmin_uniform = p.pmin_uniform;
   l.pmax = p.pmax;
   if (p.sched) {
     const bool i8 = !is_f16(kind);
@@ -193,6 +215,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.waves = p.waves;
   l.int8_kv = !is_f16(kind);
   l.fused = is_fused(kind);
+  l.nt_loads = p.nt_loads;
   l.stream = reinterpret_cast<hipStream_t>(stream);
   pa::DecodeShape& sh = l.shape;
   sh.num_seqs = num_seqs;
@@ -311,6 +334,12 @@ size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_
 pa_status_t pa_decode_set_schedule(int32_t mode) {
   if (mode < 0 || mode > 2) return PA_ERR_BAD_SHAPE;
   g_schedule_mode.store(mode, std::memory_order_relaxed);
+  return PA_OK;
+}
+
+pa_status_t pa_decode_set_load_policy(int32_t mode) {
+  if (mode < 0 || mode > 2) return PA_ERR_BAD_SHAPE;
+  g_load_mode.store(mode, std::memory_order_relaxed);
   return PA_OK;
 }
 

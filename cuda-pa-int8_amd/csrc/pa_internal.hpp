@@ -60,6 +60,7 @@ struct DecodeLaunch {
   int waves;           // waves per decode work-group: 4 or 8 (head_dim <= 128)
   bool int8_kv;
   bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
+  bool nt_loads;       // non-temporal cache-tile loads (one head chunk per kv head)
   DecodeShape shape;
   // In-kernel schedule (sched = true): `groups` resident work-groups claim
   // (row, kv head) items; the partials hold `rows_max` slot rows.
@@ -67,6 +68,7 @@ struct DecodeLaunch {
   int groups;
   int rows_max;
   int pmin, pmax;      // partition bounds, multiples of 64 (equal when forced)
+  int pmin_uniform;    // lower bound for equal lengths (<= pmin)
   int* sched_info;     // [1 + num_seqs]: partition, then the slot row base of each sequence
   uint32_t* queue;     // 8 claim counters, zero between launches
   hipStream_t stream;

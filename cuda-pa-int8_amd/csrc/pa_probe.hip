@@ -5,10 +5,12 @@
 //
 // Both probes keep several independent 16-byte loads per lane in flight and
 // fold every loaded word into a checksum, so the compiler can neither narrow
-// nor drop a load.
+// nor drop a load.  They load with the non-temporal hint, as the decode
+// kernels do.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "pa_device.hpp"
 #include "pa_mi355x.h"
 
 namespace {
@@ -17,6 +19,7 @@ constexpr int kProbeThreads = 256;
 constexpr int kUnroll = 4;   // independent 16-B loads per lane per step
 
 __device__ __forceinline__ uint32_t fold(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+__device__ __forceinline__ uint4 ld(const uint4* p) { return pa::load_stream<uint4>(p); }
 
 __global__ void __launch_bounds__(kProbeThreads)
 probe_read_contiguous(const uint4* __restrict__ p, size_t n16, uint32_t* __restrict__ sink) {
@@ -26,12 +29,12 @@ probe_read_contiguous(const uint4* __restrict__ p, size_t n16, uint32_t* __restr
   for (; i + (kUnroll - 1) * kProbeThreads < n16; i += step) {
     uint4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = p[i + u * kProbeThreads];
+    for (int u = 0; u < kUnroll; ++u) v[u] = ld(p + i + u * kProbeThreads);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);
   }
   for (int u = 0; u < kUnroll; ++u)   // ragged end of the sweep
-    if (i + u * kProbeThreads < n16) acc ^= fold(p[i + u * kProbeThreads]);
+    if (i + u * kProbeThreads < n16) acc ^= fold(ld(p + i + u * kProbeThreads));
   if (acc == 0x9E3779B9u) sink[0] = acc;   // keeps the loads live; practically never taken
 }
 
@@ -53,7 +56,7 @@ probe_read_chunks(const uint4* __restrict__ p, const int32_t* __restrict__ order
       for (int j = 0; j < c16; j += 64 * kUnroll) {
         uint4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = q[j + 64 * u];
+        for (int u = 0; u < kUnroll; ++u) v[u] = ld(q + j + 64 * u);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);
       }
@@ -67,7 +70,7 @@ probe_read_chunks(const uint4* __restrict__ p, const int32_t* __restrict__ order
         const int e = 64 * u + lane;          // 16-B element of this step
         const int b = b0 + e / c16;
         const int32_t c = b < nchunk ? order[b] : -1;
-        v[u] = (uint32_t)c < (uint32_t)total ? p[(size_t)c * c16 + e % c16] : make_uint4(0, 0, 0, 0);
+        v[u] = (uint32_t)c < (uint32_t)total ? ld(p + (size_t)c * c16 + e % c16) : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) acc ^= fold(v[u]);

@@ -148,13 +148,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(void* base, uint32_t
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
 }
 
-// Inputs are read once: non-temporal loads keep them from displacing the L2.
-__device__ __forceinline__ uint4 load_stream16(const void* p) {
-  typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
-  const u4v_t t = __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
-  return make_uint4(t[0], t[1], t[2], t[3]);
-}
-
 // The 16-B input groups of one job for one lane, and the lane's token slot.
 template <int D>
 struct QuantJob {
@@ -197,7 +190,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     const half_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
                              : key + (int64_t)tc * kts + (int64_t)h * khs;
 #pragma unroll
-    for (int j = 0; j < JQ; ++j) J.x[j] = load_stream16(src + (qq + 4 * j) * 8);
+    for (int j = 0; j < JQ; ++j) J.x[j] = load_stream<uint4>(src + (qq + 4 * j) * 8);   // read once
   };
 
   // Two jobs stay in flight ahead of the one being quantized.  A prefetch

@@ -124,6 +124,13 @@ pa_status_t pa_decode_set_waves_per_group(int32_t waves);
  * workspace. */
 pa_status_t pa_decode_set_schedule(int32_t mode);
 
+/* Tuning hook (no reference counterpart): how later decode calls in this
+ * process load K/V cache tiles.  0 = automatic: non-temporal loads when each
+ * kv head's tiles are read by one work-group (query heads per kv head <= 16),
+ * plain loads when several head chunks share them through the L2; 1 = plain;
+ * 2 = non-temporal.  Results do not depend on it. */
+pa_status_t pa_decode_set_load_policy(int32_t mode);
+
 /* FP16 KV, single launch.  Replaces paged_decode_attn_warp
  * (kernels/paged_attention_v3_warp.cu:137-176; bound at kernels/bindings.cpp:50-51).
  * When the (seq, kv-head group) units alone cannot fill the GPU the launch
