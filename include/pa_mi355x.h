@@ -126,9 +126,11 @@ pa_status_t pa_decode_set_schedule(int32_t mode);
 
 /* Tuning hook (no reference counterpart): how later decode calls in this
  * process load K/V cache tiles.  0 = automatic: non-temporal loads when each
- * kv head's tiles are read by one work-group (query heads per kv head <= 16),
- * plain loads when several head chunks share them through the L2; 1 = plain;
- * 2 = non-temporal.  Results do not depend on it. */
+ * kv head's tiles are read by one work-group (query heads per kv head <= 16)
+ * and the call reads more than 32 MB of K/V; plain loads when several head
+ * chunks share the tiles through the L2, or when a small cache may still sit
+ * in the Infinity Cache from an earlier call; 1 = plain; 2 = non-temporal.
+ * Results do not depend on it. */
 pa_status_t pa_decode_set_load_policy(int32_t mode);
 
 /* FP16 KV, single launch.  Replaces paged_decode_attn_warp
