@@ -179,6 +179,13 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
 
   const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
                            max_blocks, max_context_len, partition_tokens);
+  if (!p.sched) {
+    // The grid form launches (sequence, split) items rounded up to groups of 8,
+    // times the kv heads and head chunks; a dispatch counts work-items in 32 bits.
+    const long long items = (long long)num_seqs * p.nsplit;
+    const long long groups = (items + 7) / 8 * 8 * num_kv_heads * p.nchunk;
+    if (groups * p.waves * 64 > 0xFFFFFFFFll) return PA_ERR_BAD_SHAPE;
+  }
   const WsLayout wl = ws_layout(p, head_dim, num_seqs);
   if (!workspace || workspace_bytes < wl.total) return PA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0) return PA_ERR_WORKSPACE;
@@ -230,7 +237,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   sh.max_blocks = max_blocks;
   sh.partition = p.partition;
   sh.nsplit = p.nsplit;
-  sh.num_items = num_seqs * num_kv_heads * p.nsplit;
+  sh.num_items = num_seqs * p.nsplit;
   sh.scale_log2 = scale * 1.4426950408889634f;
 
   hipError_t e;

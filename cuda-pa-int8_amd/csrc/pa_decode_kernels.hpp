@@ -789,18 +789,36 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
   static_assert(sizeof(DecodeSmem<D, NW>) * (kWavesPerCU / NW) <= kLdsPerCU, "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
 
-  // ---- work item (XCD-aware: the head chunks of one item share blockIdx % 8)
+  // ---- work item (XCD-aware).  With at least 8 (sequence, split) items, an
+  // item's kv heads and head chunks get work-group indices 8 apart, so they
+  // share blockIdx % 8 (their XCD under round-robin dispatch), run at about
+  // the same time and meet in that XCD's L2: they read the same block-table
+  // lines, the head chunks of a kv head the same K/V tiles, and with INT8 all
+  // kv heads of a block the same scale lines (the block's scales are
+  // adjacent).  With fewer items that would leave XCDs idle, so the kv heads
+  // are spread over the XCDs and only the head chunks are grouped.
   const int wg = blockIdx.x;
-  const int per_grp = 8 * sh.nchunk;
-  const int grp = wg / per_grp;
-  const int rem = wg - grp * per_grp;
-  const int chunk = rem >> 3;
-  const int item = grp * 8 + (rem & 7);
-  if (item >= sh.num_items) return;
-  const int split = item % sh.nsplit;
-  const int sk = item / sh.nsplit;
-  const int kvh = sk % sh.num_kv_heads;
-  const int seq = sk / sh.num_kv_heads;
+  const bool by_item = sh.num_items >= 8;
+  const int per = by_item ? sh.num_kv_heads * sh.nchunk : sh.nchunk;
+  const int grp = wg / (8 * per);
+  const int rem = wg - grp * 8 * per;
+  const int sub = rem >> 3;
+  const int idx = grp * 8 + (rem & 7);
+  int seq, kvh, chunk, split;
+  if (by_item) {
+    if (idx >= sh.num_items) return;
+    split = idx % sh.nsplit;
+    seq = idx / sh.nsplit;
+    kvh = sub / sh.nchunk;
+    chunk = sub - kvh * sh.nchunk;
+  } else {
+    if (idx >= sh.num_items * sh.num_kv_heads) return;
+    split = idx % sh.nsplit;
+    const int sk = idx / sh.nsplit;
+    kvh = sk % sh.num_kv_heads;
+    seq = sk / sh.num_kv_heads;
+    chunk = sub;
+  }
 
   // Contexts are clamped to what the block table holds and to what the grid's
   // splits cover, so no work-group reads past the table or the partials.
@@ -1172,7 +1190,11 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
         l.part_acc, l.part_ml, l.context_lens, l.sched_info, out, sh, l.rows_max);
     return hipGetLastError();
   }
-  const int grid = ((sh.num_items + 7) / 8) * 8 * sh.nchunk;
+  // Groups of 8 items with their kv heads and head chunks, or, below 8 items,
+  // of 8 (item, kv head) pairs with their head chunks (see decode_kernel).
+  const int grid = sh.num_items >= 8
+                       ? (sh.num_items + 7) / 8 * 8 * sh.num_kv_heads * sh.nchunk
+                       : (sh.num_items * sh.num_kv_heads + 7) / 8 * 8 * sh.nchunk;
   const auto* q = static_cast<const half_t*>(l.q);
   const auto* kc = static_cast<const uint8_t*>(l.k_cache);
   const auto* vc = static_cast<const uint8_t*>(l.v_cache);

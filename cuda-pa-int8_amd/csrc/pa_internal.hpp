@@ -29,7 +29,7 @@ constexpr int kSchedQueueStride = 32;   // words between the 8 claim counters (1
 // block-id and context-length loads without first fetching its arguments.
 struct DecodeShape {
   int nchunk;       // group / head_tile
-  int num_items;    // num_seqs * num_kv_heads * nsplit
+  int num_items;    // num_seqs * nsplit: (sequence, split) items of the grid form
   int nsplit;       // splits present in the grid
   int num_kv_heads;
   int partition;    // tokens per split, multiple of kIterTokens
