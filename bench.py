@@ -7,7 +7,9 @@ head_dim 128, 32 sequences x 4096 tokens, FP16 KV, single-launch kernel.
 ``value`` is its algorithmic HBM bytes per step / time per step (GB/s).
 The other BASELINE configs are measured the same way and reported under
 ``configs`` (INT8 vs FP16, long-context split-K, ragged serving mix,
-quantize + cache-write, the tiny CPU-runnable case).
+quantize + cache-write, the tiny CPU-runnable case), next to a dense
+baseline (SDPA over K/V gathered into contiguous tensors, as the
+reference's bench_paged_decode.py:131-145 does).
 
 Timing: W eager warm-up steps, then the K steps are captured in one HIP
 graph (each step reads a different copy of the cache when one copy would
@@ -36,7 +38,7 @@ for _p in (ROOT, PKG_ROOT):
 
 METRIC = "decode µs + achieved HBM GB/s (% of peak), FP16 vs INT8 KV, GQA 12/2 d128"
 MALL_BYTES = 256 << 20
-ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "ceiling"]
+ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "dense", "ceiling"]
 
 
 def log(*a):
@@ -251,6 +253,80 @@ def run_quant_write(torch, steps, warmup, seed=0):
     return res
 
 
+def gather_dense(torch, case, lens, num_heads):
+    """Contiguous fp16 K/V [S, H, ctx, D] gathered from the first paged cache
+    copy through the block tables, repeated over the GQA group (equal lengths)."""
+    kc, vc = case["caches"][0][0], case["caches"][0][1]
+    bt = case["bt"]
+    S, ctx = len(lens), lens[0]
+    nblk = (ctx + case["bs"] - 1) // case["bs"]
+    ids = bt[:, :nblk].long()                                    # [S, nblk]
+    k = kc[ids]                                                  # [S, nblk, Hkv, D/8, bs, 8]
+    k = k.permute(0, 2, 1, 4, 3, 5).reshape(S, kc.shape[1], nblk * case["bs"], -1)
+    v = vc[ids]                                                  # [S, nblk, Hkv, D, bs]
+    v = v.permute(0, 2, 1, 4, 3).reshape(S, vc.shape[1], nblk * case["bs"], -1)
+    k, v = k[:, :, :ctx].contiguous(), v[:, :, :ctx].contiguous()
+    rep = num_heads // kc.shape[1]
+    if rep > 1:
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+    return k, v
+
+
+def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=False):
+    """Dense attention over gathered, GQA-repeated K/V (the reference's SDPA
+    ceiling, bench_paged_decode.py:131-145), timed with plain launches next to
+    the paged kernel on the same inputs.  SDPA runs on its flash or
+    memory-efficient backend; if neither takes the shape, an fp16 matmul form
+    over contiguous operands stands in (named in the result)."""
+    import pa_int8
+    from pa_int8 import metrics
+
+    case = make_case(torch, lens, h, hkv, d, 16, "cuda", 0, False, outliers, 1)
+    k, v = gather_dense(torch, case, lens, h)
+    q = case["q"].unsqueeze(2)                                   # [S, H, 1, D]
+    scale = case["scale"]
+    impl = "sdpa"
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        def dense():
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
+        ref = dense()
+        torch.cuda.synchronize()
+    except RuntimeError:
+        impl = "fp16 matmul (q k^T, softmax in fp32, p v), contiguous operands"
+        kt = k.transpose(-1, -2).contiguous()
+
+        def dense():
+            p = torch.softmax(torch.matmul(q, kt).float() * scale, dim=-1).to(torch.float16)
+            return torch.matmul(p, v)
+        ref = dense()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        dense()
+    ms_dense = time_eager(torch, [dense], steps)
+    out = torch.empty_like(case["q"])
+    pa_int8.decode("warp", out, case["q"], case["caches"][0][0], case["caches"][0][1],
+                   case["bt"], case["ctx"], scale, 16)
+    torch.cuda.synchronize()
+    diff = (out.float() - ref.squeeze(2).float()).abs().max().item()
+    dense_bytes = 2 * k.numel() * k.element_size() + 2 * q.numel() * 2
+    paged_bytes = metrics.decode_bytes(lens, h, hkv, d, kv_elem_bytes=2, scales=False)
+    res = dict(impl=impl, us=round(ms_dense * 1e3, 2), bytes_read=dense_bytes,
+               gbs=round(dense_bytes / (ms_dense * 1e-3) / 1e9, 1),
+               paged_algo_bytes=paged_bytes,
+               max_abs_diff_vs_paged_warp=round(diff, 6), seqs=len(lens), heads=f"{h}/{hkv}",
+               context=lens[0], steps=steps,
+               note="K/V gathered and repeated over the GQA group outside the timed region")
+    log(f"[bench] {name} dense baseline ({impl}): {res['us']} us "
+        f"({res['gbs']} GB/s over {dense_bytes} B read); max |dense - paged| {diff:.2e}")
+    del case, k, v, q
+    torch.cuda.empty_cache()
+    return res
+
+
 def lognormal_lens(n, seed):
     import numpy as np
 
@@ -300,6 +376,12 @@ def run_configs(torch, names, steps, warmup):
         out["cfg5_lens"] = dict(n=256, median=int(np.median(lens)), mean=float(np.mean(lens)),
                                 max=int(max(lens)), sigma=1.0,
                                 distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
+    if "dense" in names:
+        out["dense_cfg2_qwen_fp16"] = run_dense_baseline(torch, "cfg2", [4096] * 32, 12, 2, 128,
+                                                         steps_for(150, steps), warmup)
+        out["dense_cfg4_llama_32k_fp16"] = run_dense_baseline(
+            torch, "cfg4 32768", [32768] * 8, 32, 8, 128, steps_for(700, steps), warmup,
+            outliers=True)
     return out
 
 

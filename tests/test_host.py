@@ -237,3 +237,29 @@ def test_paged_cache_class_host_logic():
     with pytest.raises(RuntimeError, match="CUDA"):
         c.prefill(0, torch.zeros(5, 2, 128, dtype=torch.float16),
                   torch.zeros(5, 2, 128, dtype=torch.float16))
+
+
+def test_bench_dense_gather_inverts_the_paged_layout():
+    """bench.gather_dense (the dense baseline's input) recovers the contiguous
+    K/V that the oracle's builder scattered into the paged layout, repeated
+    over the GQA group."""
+    import sys
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    from oracle import paged_decode_ref as ref
+
+    rng = np.random.default_rng(3)
+    s, ctx, hkv, h, d, bs = 3, 40, 2, 6, 16, 16
+    k = rng.standard_normal((s, ctx, hkv, d)).astype(np.float16)
+    v = rng.standard_normal((s, ctx, hkv, d)).astype(np.float16)
+    kc, vc, bt = ref.build_paged_kv_cache(k, v, np.full(s, ctx), block_size=bs, rng=rng)
+    case = dict(caches=[(torch.from_numpy(kc), torch.from_numpy(vc), None, None)],
+                bt=torch.from_numpy(bt.astype(np.int32)), bs=bs)
+    kd, vd = bench.gather_dense(torch, case, [ctx] * s, h)
+    assert kd.shape == (s, h, ctx, d) and vd.shape == (s, h, ctx, d)
+    want_k = np.repeat(k.transpose(0, 2, 1, 3), h // hkv, axis=1)
+    want_v = np.repeat(v.transpose(0, 2, 1, 3), h // hkv, axis=1)
+    assert np.array_equal(kd.numpy(), want_k) and np.array_equal(vd.numpy(), want_v)
