@@ -38,7 +38,7 @@ for _p in (ROOT, PKG_ROOT):
 
 METRIC = "decode µs + achieved HBM GB/s (% of peak), FP16 vs INT8 KV, GQA 12/2 d128"
 MALL_BYTES = 256 << 20
-ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "dense", "ceiling"]
+ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "dense", "e2e", "ceiling"]
 
 
 def log(*a):
@@ -327,6 +327,68 @@ def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=Fal
     return res
 
 
+def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0):
+    """End-to-end greedy decode of a random-init Qwen2.5-1.5B-shape model (fp16,
+    28 layers, 12 q / 2 kv heads, head_dim 128, vocab 151936) through the
+    transformers bridge: prompt attention by SDPA, every decode step's
+    attention by the split-K kernel over the paged cache (reference:
+    benchmarks/int8_bridge/run_bridge.py).  Per cache variant: time to first
+    token, time per output token, KV-cache bytes, and agreement with the FP16
+    variant (greedy match; mean |log p| difference on the FP16 continuation,
+    teacher-forced).  No checkpoint is available offline, so perplexity itself
+    is not meaningful here and is not reported."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from pa_int8 import PagedKVCache
+    from pa_int8 import qwen_bridge as br
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
+                      max_position_embeddings=32768, rope_theta=1e6, tie_word_embeddings=True)
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg).to(torch.float16).eval()
+    br.register()
+    model.set_attn_implementation(br.ATTN_NAME)
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g).cuda()
+    warm = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128, max_len=prompt_len + 16,
+                        variant="fp16")
+    br.generate_greedy(model, prompt, 16, warm)                 # first-use costs of every op
+    del warm
+    res = {}
+    ref_tokens = ref_lp = None
+    for variant in ("fp16", "int8_per_token", "int8_per_tensor"):
+        cache = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128,
+                             max_len=prompt_len + max_new, variant=variant)
+        br.generate_greedy(model, prompt, 4, cache)             # warm-up
+        gen, ttft, tpot, _ = br.generate_greedy(model, prompt, max_new, cache)
+        if ref_tokens is None:
+            ref_tokens = gen
+        lp = torch.tensor(br.teacher_force_logprobs(model, prompt, ref_tokens, cache))
+        if ref_lp is None:
+            ref_lp = lp
+        res[variant] = dict(ttft_ms=round(ttft * 1e3, 2), tpot_ms=round(tpot * 1e3, 3),
+                            kv_bytes=int(cache.kv_bytes_for_len(prompt_len + max_new)),
+                            greedy_match_vs_fp16=round(float((gen == ref_tokens).float().mean()), 4),
+                            mean_abs_dlogp_vs_fp16=round(float((lp - ref_lp).abs().mean()), 5))
+        log(f"[bench] e2e bridge {variant}: TTFT {res[variant]['ttft_ms']} ms, "
+            f"TPOT {res[variant]['tpot_ms']} ms, greedy match {res[variant]['greedy_match_vs_fp16']}")
+        del cache
+    res["setup"] = dict(model="random-init Qwen2.5-1.5B shape (no checkpoint offline), fp16",
+                        prompt_len=prompt_len, max_new=max_new, batch=1,
+                        decode_attention="split-K kernel via transformers AttentionInterface",
+                        timing="wall clock per model call, synchronized, eager launches "
+                               "(the 28 layers' host-side launch overhead dominates TPOT)",
+                        agreement="random weights give nearly flat logits, so one early argmax "
+                                  "flip changes every later greedy token: greedy_match is "
+                                  "informational; mean_abs_dlogp (teacher-forced on the FP16 "
+                                  "continuation) measures the quantization error")
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def lognormal_lens(n, seed):
     import numpy as np
 
@@ -376,6 +438,8 @@ def run_configs(torch, names, steps, warmup):
         out["cfg5_lens"] = dict(n=256, median=int(np.median(lens)), mean=float(np.mean(lens)),
                                 max=int(max(lens)), sigma=1.0,
                                 distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
+    if "e2e" in names:
+        out["e2e_qwen_bridge"] = run_e2e_bridge(torch)
     if "dense" in names:
         out["dense_cfg2_qwen_fp16"] = run_dense_baseline(torch, "cfg2", [4096] * 32, 12, 2, 128,
                                                          steps_for(150, steps), warmup)

@@ -1,0 +1,99 @@
+"""The transformers bridge on the GPU (counterpart of the reference's gate 2,
+tests/test_int8_bridge.py:131-185, which needs Qwen weights that are not
+available offline): a random-init Qwen2 with the Qwen2.5-1.5B attention shape
+runs prompt + decode through the paged cache and the split-K kernels, and its
+per-token log-probabilities are compared with the same model's dense fp32
+attention (``reference_attention``) on the same tokens."""
+
+import numpy as np
+import pytest
+import torch
+
+from _qwen import LOGP_MAX, tiny_qwen
+
+pytestmark = pytest.mark.gpu
+transformers = pytest.importorskip("transformers")
+
+
+def _tokens(n, seed, vocab=512):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (1, n), generator=g).cuda()
+
+
+@pytest.fixture(scope="module")
+def model():
+    from pa_int8 import qwen_bridge as br
+
+    br.register()
+    return tiny_qwen(dtype=torch.float16, device="cuda")
+
+
+def _bridge_logprobs(model, prompt, cont, variant):
+    from pa_int8 import PagedKVCache
+    from pa_int8 import qwen_bridge as br
+
+    model.set_attn_implementation(br.ATTN_NAME)
+    cfg = model.config
+    cache = PagedKVCache(num_layers=cfg.num_hidden_layers, num_kv_heads=cfg.num_key_value_heads,
+                         head_dim=cfg.hidden_size // cfg.num_attention_heads,
+                         max_len=prompt.shape[1] + cont.shape[1], variant=variant)
+    return np.array(br.teacher_force_logprobs(model, prompt, cont, cache)), cache
+
+
+def _reference_logprobs(model, prompt, cont):
+    from pa_int8 import qwen_bridge as br
+
+    model.set_attn_implementation(br.REFERENCE_ATTN_NAME)
+    return np.array(br.reference_logprobs(model, prompt, cont))
+
+
+@pytest.mark.parametrize("plen,n", [(40, 24), (301, 8), (16, 17)])
+def test_fp16_bridge_matches_dense_reference(model, plen, n):
+    prompt, cont = _tokens(plen, plen), _tokens(n, plen + 1)
+    got, cache = _bridge_logprobs(model, prompt, cont, "fp16")
+    want = _reference_logprobs(model, prompt, cont)
+    err = np.abs(got - want)
+    print(f"fp16 bridge, prompt {plen} + {n}: max |dlogp| {err.max():.2e}, mean {err.mean():.2e}")
+    assert err.max() < LOGP_MAX
+    # every continuation token is fed (the last one's logits are unused): plen + n cached
+    assert cache.lengths == [plen + n] * model.config.num_hidden_layers
+
+
+def test_greedy_generation_follows_the_reference(model):
+    """Every token the bridge generates greedily is the reference's argmax at
+    that position, wherever the reference's top-2 margin is clear."""
+    from pa_int8 import PagedKVCache
+    from pa_int8 import qwen_bridge as br
+
+    prompt = _tokens(33, 7)
+    model.set_attn_implementation(br.ATTN_NAME)
+    cfg = model.config
+    cache = PagedKVCache(num_layers=cfg.num_hidden_layers, num_kv_heads=cfg.num_key_value_heads,
+                         head_dim=128, max_len=33 + 20, variant="fp16")
+    gen, ttft, tpot, steps = br.generate_greedy(model, prompt, 20, cache)
+    assert gen.shape == (1, 20) and ttft > 0 and tpot > 0 and len(steps) == 20
+    model.set_attn_implementation(br.REFERENCE_ATTN_NAME)
+    ids = torch.cat([prompt, gen[:, :-1]], dim=1)
+    with torch.no_grad():
+        logits = model(input_ids=ids, use_cache=False).logits[0, 32:].float()
+    top2 = logits.topk(2, dim=-1)
+    clear = (top2.values[:, 0] - top2.values[:, 1]) > 0.05
+    agree = top2.indices[:, 0] == gen[0]
+    assert bool((agree | ~clear).all()), (agree.cpu().tolist(), clear.cpu().tolist())
+    assert int(clear.sum()) >= 10
+
+
+def test_int8_bridges_track_fp16(model):
+    """INT8 caches (per token, per tensor) against the FP16 bridge on the same
+    tokens; per-token scales are at least as close as one per-tensor scale."""
+    prompt, cont = _tokens(64, 11), _tokens(32, 12)
+    fp, _ = _bridge_logprobs(model, prompt, cont, "fp16")
+    err = {}
+    for variant in ("int8_per_token", "int8_per_tensor"):
+        lp, _ = _bridge_logprobs(model, prompt, cont, variant)
+        err[variant] = np.abs(lp - fp)
+        print(f"{variant}: max |dlogp| vs fp16 {err[variant].max():.3e}, "
+              f"mean {err[variant].mean():.3e}")
+    assert err["int8_per_token"].max() < 0.5
+    assert err["int8_per_token"].mean() < 0.1
+    assert err["int8_per_token"].mean() <= err["int8_per_tensor"].mean() * 1.1 + 1e-3
