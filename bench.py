@@ -352,29 +352,31 @@ def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0):
     model.set_attn_implementation(br.ATTN_NAME)
     g = torch.Generator().manual_seed(seed)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g).cuda()
-    warm = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128, max_len=prompt_len + 16,
-                        variant="fp16")
-    br.generate_greedy(model, prompt, 16, warm)                 # first-use costs of every op
-    del warm
     res = {}
     ref_tokens = ref_lp = None
-    for variant in ("fp16", "int8_per_token", "int8_per_tensor"):
-        cache = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128,
-                             max_len=prompt_len + max_new, variant=variant)
-        br.generate_greedy(model, prompt, 4, cache)             # warm-up
-        gen, ttft, tpot, _ = br.generate_greedy(model, prompt, max_new, cache)
-        if ref_tokens is None:
-            ref_tokens = gen
-        lp = torch.tensor(br.teacher_force_logprobs(model, prompt, ref_tokens, cache))
-        if ref_lp is None:
-            ref_lp = lp
-        res[variant] = dict(ttft_ms=round(ttft * 1e3, 2), tpot_ms=round(tpot * 1e3, 3),
-                            kv_bytes=int(cache.kv_bytes_for_len(prompt_len + max_new)),
-                            greedy_match_vs_fp16=round(float((gen == ref_tokens).float().mean()), 4),
-                            mean_abs_dlogp_vs_fp16=round(float((lp - ref_lp).abs().mean()), 5))
-        log(f"[bench] e2e bridge {variant}: TTFT {res[variant]['ttft_ms']} ms, "
-            f"TPOT {res[variant]['tpot_ms']} ms, greedy match {res[variant]['greedy_match_vs_fp16']}")
-        del cache
+    # two passes over the variants; the first pays one-time costs (kernel loads, clock
+    # ramp: a first FP16 pass measured 18.8 ms per token, later passes 13.3 ms)
+    for rep in range(2):
+        for variant in ("fp16", "int8_per_token", "int8_per_tensor"):
+            cache = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128,
+                                 max_len=prompt_len + max_new, variant=variant)
+            gen, ttft, tpot, _ = br.generate_greedy(model, prompt, max_new, cache)
+            if rep == 0:
+                continue
+            if ref_tokens is None:
+                ref_tokens = gen
+            lp = torch.tensor(br.teacher_force_logprobs(model, prompt, ref_tokens, cache))
+            if ref_lp is None:
+                ref_lp = lp
+            res[variant] = dict(
+                ttft_ms=round(ttft * 1e3, 2), tpot_ms=round(tpot * 1e3, 3),
+                kv_bytes=int(cache.kv_bytes_for_len(prompt_len + max_new)),
+                greedy_match_vs_fp16=round(float((gen == ref_tokens).float().mean()), 4),
+                mean_abs_dlogp_vs_fp16=round(float((lp - ref_lp).abs().mean()), 5))
+            log(f"[bench] e2e bridge {variant}: TTFT {res[variant]['ttft_ms']} ms, "
+                f"TPOT {res[variant]['tpot_ms']} ms, mean |dlogp| vs fp16 "
+                f"{res[variant]['mean_abs_dlogp_vs_fp16']}")
+            del cache
     res["setup"] = dict(model="random-init Qwen2.5-1.5B shape (no checkpoint offline), fp16",
                         prompt_len=prompt_len, max_new=max_new, batch=1,
                         decode_attention="split-K kernel via transformers AttentionInterface",

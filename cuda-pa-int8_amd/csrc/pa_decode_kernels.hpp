@@ -355,8 +355,13 @@ __device__ __forceinline__ void decode_split(
   // of 16 tokens, the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i, and the
   // valid tokens among the lane's 8 of each pair.
   uint4 kw[PAIRS][KC];
+  uint4 vw[NT];
+  // W8: the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i and the valid
+  // tokens among the lane's 8 of each pair.  They are loaded one iteration
+  // ahead, with the K rows, so the softmax does not wait for the V rows (the
+  // memory counter completes in order): `wa` holds the next iteration's, and
+  // each iteration copies them out before loading the following ones.
   struct W8Buf {
-    uint4 vw[NT];
     float4 ks4, vs4;
     int nvalid[PAIRS];
   };
@@ -419,27 +424,32 @@ __device__ __forceinline__ void decode_split(
     }
   };
   // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7.
+  // W8: the scales and valid counts of an iteration (see W8Buf).
+  auto issue_scales = [&](int it_, const Blocks& b, W8Buf& B) {
+    const int tg = t_begin + it_ * IT + 16 * g;
+    const int tgc = tg < t_end ? tg : t_begin;
+    const bool vok = (unsigned)b.vb[0] < (unsigned)sh.num_blocks;
+    const int vb = vok ? b.vb[0] : 0;
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int t0 = tg + 8 * p;
+      B.nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
+    }
+    const size_t slot = ((size_t)vb * hkv + kvh) * bs + (tgc & (bs - 1)) + 4 * (r & 3);
+    // (plain loads: a scale line holds several kv heads' scales)
+    B.ks4 = *reinterpret_cast<const float4*>(ksc + slot);
+    B.vs4 = *reinterpret_cast<const float4*>(vsc + slot);
+  };
   auto issue_v = [&](int it_, const Blocks& b, W8Buf& B) {
     const int tok0 = t_begin + it_ * IT;
     if constexpr (W8) {
       // V rows: dim 16t + r, tokens tok0 + 16g .. + 15 (pair p uses 8p .. 8p + 7).
       const int tg = tok0 + 16 * g;
       const int tgc = tg < t_end ? tg : t_begin;
-      const bool vok = (unsigned)b.vb[0] < (unsigned)sh.num_blocks;
-      const int vb = vok ? b.vb[0] : 0;
-      const int voff = tgc & (bs - 1);
+      const int vb = (unsigned)b.vb[0] < (unsigned)sh.num_blocks ? b.vb[0] : 0;
+      const uint8_t* vp = vc + (((size_t)vb * hkv + kvh) * D + r) * bs + (tgc & (bs - 1));
 #pragma unroll
-      for (int p = 0; p < PAIRS; ++p) {
-        const int t0 = tg + 8 * p;
-        B.nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
-      }
-      const uint8_t* vp = vc + (((size_t)vb * hkv + kvh) * D + r) * bs + voff;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) B.vw[t] = load_tile<uint4, NTL>(vp + (size_t)(16 * t) * bs);
-      const size_t slot = ((size_t)vb * hkv + kvh) * bs + voff + 4 * (r & 3);
-      // (plain loads: a scale line holds several kv heads' scales)
-      B.ks4 = *reinterpret_cast<const float4*>(ksc + slot);
-      B.vs4 = *reinterpret_cast<const float4*>(vsc + slot);
+      for (int t = 0; t < NT; ++t) vw[t] = load_tile<uint4, NTL>(vp + (size_t)(16 * t) * bs);
       return;
     }
 #pragma unroll
@@ -584,8 +594,8 @@ __device__ __forceinline__ void decode_split(
         for (int t = 0; t < NT; ++t) {
           h8_t av;
           if constexpr (W8) {
-            av = i8x8_exact(p == 0 ? make_uint2(B.vw[t].x, B.vw[t].y)
-                                   : make_uint2(B.vw[t].z, B.vw[t].w));
+            av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y)
+                                   : make_uint2(vw[t].z, vw[t].w));
           } else if constexpr (I8) {
             av = i8x8_exact(vr[p][t]);
           } else {
@@ -645,6 +655,7 @@ __device__ __forceinline__ void decode_split(
     {
       Blocks b0;
       load_blocks(w, b0);
+      if constexpr (W8) issue_scales(w, b0, wa);
       issue_k(w, b0);
       __builtin_amdgcn_sched_barrier(0);
       issue_v(w, b0, wa);
@@ -655,12 +666,17 @@ __device__ __forceinline__ void decode_split(
     qk(s);
     __builtin_amdgcn_sched_barrier(0);
     int nxt = w + NW;
+    // One iteration: the next iteration's K rows (and, W8, its scales) go out,
+    // this iteration's softmax and PV run, then the next V rows go out and
+    // the next QK runs.
     while (nxt < n_it) {
+      W8Buf cur = wa;   // W8: this iteration's scales, loaded one iteration ago
       Blocks bn;
       load_blocks(nxt, bn);
+      if constexpr (W8) issue_scales(nxt, bn, wa);
       issue_k(nxt, bn);
       __builtin_amdgcn_sched_barrier(0);
-      softmax_pv(s, mask_needed(wa), wa);
+      softmax_pv(s, mask_needed(cur), cur);
       __builtin_amdgcn_sched_barrier(0);
       issue_v(nxt, bn, wa);
       __builtin_amdgcn_sched_barrier(0);
