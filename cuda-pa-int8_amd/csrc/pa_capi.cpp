@@ -87,7 +87,7 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   if (ctx < 1) ctx = 1;
   long long part;
   // Caps the serial work of a work-group and keeps a split's block ids in LDS.
-  const long long hi = (long long)pa::kMaxPartitionPer4Waves * p.waves / 4;
+  const long long hi = (long long)pa::max_partition_per_4_waves(head_dim) * p.waves / 4;
   if (partition_tokens > 0) {
     part = std::min<long long>(partition_tokens, hi);
   } else {

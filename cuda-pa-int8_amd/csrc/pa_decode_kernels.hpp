@@ -197,11 +197,11 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
   }
 }
 
-// Block ids of one split: at most kMaxPartitionPer4Waves * NW / 4 tokens,
+// Block ids of one split: at most max_partition_per_4_waves(D) * NW / 4 tokens,
 // starting anywhere inside a block of >= kMinBlockSize tokens.
-template <int NW>
+template <int D, int NW>
 constexpr int split_blocks_max() {
-  return kMaxPartitionPer4Waves * NW / 4 / kMinBlockSize + 1;
+  return max_partition_per_4_waves(D) * NW / 4 / kMinBlockSize + 1;
 }
 
 // Row padding of the wave-merge slots: lane (r, g) touches row r, so rows
@@ -217,7 +217,7 @@ struct alignas(16) DecodeSmem {
   float a[NW][16][D + kMergeRowPad];   // each wave's accumulator: per head, per dim (+ pad)
   float m[NW][16];
   float l[NW][16];
-  int blk[split_blocks_max<NW>()];     // the split's block ids
+  int blk[split_blocks_max<D, NW>()];     // the split's block ids
   int last;
 };
 
@@ -290,9 +290,9 @@ __device__ __forceinline__ void decode_split(
   // block the split can touch and are issued before the context length is
   // known, so the two memory round trips overlap.
   const int b_first = t_begin >> bsl;
-  constexpr int kStageRegs = (split_blocks_max<NW>() + NW * kWave - 1) / (NW * kWave);
+  constexpr int kStageRegs = (split_blocks_max<D, NW>() + NW * kWave - 1) / (NW * kWave);
   int nstage = min(((t_begin + wk.partition - 1) >> bsl) - b_first + 1, sh.max_blocks - b_first);
-  nstage = nstage < 0 ? 0 : min(nstage, split_blocks_max<NW>());
+  nstage = nstage < 0 ? 0 : min(nstage, split_blocks_max<D, NW>());
   int staged[kStageRegs];
 #pragma unroll
   for (int k = 0; k < kStageRegs; ++k) {

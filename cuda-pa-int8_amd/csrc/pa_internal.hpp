@@ -12,7 +12,11 @@ constexpr int kIterTokens = 64;      // partition granularity (one wave iteratio
 constexpr int kMaxGroupTile = 16;    // query heads sharing one KV read (one MFMA column tile)
 // Largest split, per 4 waves of a work-group.  The planner never exceeds it
 // (forced partitions included), so the block ids of one split fit in LDS.
-constexpr int kMaxPartitionPer4Waves = 4096;
+// 8192 rather than 4096 for head_dim <= 128: uniform long contexts get half
+// as many items per work-group, each paying its start once (MI355X, bench
+// config 4 INT8 64k / 128k: 189.9 -> 185.9 us / 369.6 -> 362.8 us).  With
+// head_dim 256 the larger block list would not fit two 4-wave groups per CU.
+constexpr int max_partition_per_4_waves(int head_dim) { return head_dim > 128 ? 4096 : 8192; }
 constexpr int kMinBlockSize = 8;
 // In-kernel scheduling (persistent work-groups over a compact work list):
 // the lengths of up to kSchedMaxSeqs sequences are staged in LDS; a ragged

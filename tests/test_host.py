@@ -98,18 +98,20 @@ def test_plan_invariants(lib, s, h, hkv, ctx):
 
 
 def test_forced_partition_is_capped(lib):
-    # a split holds at most 1024 tokens per wave of the work-group (its block
-    # ids are staged in LDS): 8192 at 8 waves (head_dim <= 128), 4096 at 4
+    # a split holds at most 2048 tokens per wave of the work-group for
+    # head_dim <= 128 and 1024 for head_dim 256 (its block ids are staged in
+    # LDS): FP16 split-K with one head chunk runs 8 waves (16384 tokens),
+    # head_dim 256 and INT8 split-K run 4 (4096 / 8192)
     part, ns = ctypes.c_int32(), ctypes.c_int32()
-    for d, cap in ((128, 8192), (64, 8192), (256, 4096)):
-        assert lib.pa_decode_plan(1, 8, 32, d, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
+    for kind, d, cap in ((1, 128, 16384), (1, 64, 16384), (1, 256, 4096), (3, 128, 8192)):
+        assert lib.pa_decode_plan(kind, 8, 32, d, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
                                   ctypes.byref(ns)) == 0
-        assert part.value == cap and ns.value == 131072 // cap
+        assert part.value == cap and ns.value == 131072 // cap, (kind, d, part.value)
     lib.pa_decode_set_waves_per_group(4)
     try:
         assert lib.pa_decode_plan(1, 8, 32, 128, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
                                   ctypes.byref(ns)) == 0
-        assert part.value == 4096
+        assert part.value == 8192
     finally:
         lib.pa_decode_set_waves_per_group(0)
 
