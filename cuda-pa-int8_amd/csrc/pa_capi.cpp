@@ -103,9 +103,10 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   p.partition = (int)part;
   p.nsplit = (int)((ctx + part - 1) / part);
 
-  // Cache-tile loads: non-temporal when every K/V byte is read by exactly one
+  // V-row loads: non-temporal when every K/V byte is read by exactly one
   // work-group (one head chunk per kv head); MI355X streams them faster (FP16
-  // config 3: 94 -> 84 us, config 4 32k: 184 -> 166 us).  With several head
+  // config 3: 94 -> 84 us, config 4 32k: 184 -> 166 us, when K took the same
+  // policy; K rows now always load plain, see load_tile).  With several head
   // chunks per kv head the chunks find the tiles in the L2 only with plain
   // loads (MQA 32/1 of config 5: 71 us plain, 95 us non-temporal).
   // A launch that reads little (bound: every sequence at `ctx` tokens) is
