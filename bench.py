@@ -114,11 +114,17 @@ def copies_for(bytes_per_copy):
 
 # --------------------------------------------------------------------------- timing
 
+EAGER_ONLY = False   # --eager: every measurement uses plain launches
+
+
 def time_steps(torch, step_fns, steps, warmup, replays=1):
-    """Median ms per step over `replays` timed graph replays of `steps` steps."""
+    """Median ms per step over `replays` timed graph replays of `steps` steps
+    (with --eager: `steps` plain launches after `warmup` ones)."""
     n = len(step_fns)
     for i in range(warmup):
         step_fns[i % n]()
+    if EAGER_ONLY:
+        return time_eager(torch, step_fns, steps)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -535,7 +541,19 @@ def cpu_baseline(seconds):
                         f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32) in "
                         f"{dt:.1f} s; {seq_ms:.2f} ms per sequence, "
                         f"{seq_ms * 32:.1f} ms per 32-sequence step"),
-                host_cpus=os.cpu_count())
+                host_cpus=os.cpu_count(), cpu_model=_cpu_model())
+
+
+def _cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 # --------------------------------------------------------------------------- main
@@ -550,7 +568,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
-                    help="time the headline with plain launches instead of a HIP graph "
+                    help="time every measurement with plain launches instead of a HIP graph "
                          "(used under rocprofv3 counter collection)")
     ap.add_argument("--pmc-copy", action="store_true",
                     help="also run a 256 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -572,6 +590,8 @@ def main():
 
     pa_int8.ext()
     names = ALL_CONFIGS if args.configs == "all" else args.configs.split(",")
+    global EAGER_ONLY
+    EAGER_ONLY = args.eager
 
     # ---- headline: config 2, single-launch FP16
     lens = [4096] * 32
