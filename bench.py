@@ -499,7 +499,31 @@ def read_ceiling(torch, sizes=(134_217_728, 1_073_741_824)):
         del bufs
         torch.cuda.empty_cache()
         log(f"[bench] read ceiling at {nbytes} B: {res}")
+    out["read_write_1gib"] = read_write_ceiling(torch)
     return out
+
+
+def read_write_ceiling(torch, nbytes=1 << 30):
+    """Mixed read + write rates of torch's own copy kernels (the roof the
+    write kernel shares): a same-dtype copy (1 byte read per byte written)
+    and an fp16 -> int8 conversion (2 : 1, the write kernel's ratio), each
+    moving about nbytes per step.  GB/s of bytes read plus bytes written."""
+    res = {}
+    n_copy = nbytes // 2
+    src = torch.ones(n_copy, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ms = time_steps(torch, [lambda: dst.copy_(src)], 20, 4, 3)
+    res["copy_1to1_gbs"] = round(2 * n_copy / (ms * 1e-3) / 1e9, 1)
+    del src, dst
+    n_conv = nbytes // 3
+    src = torch.ones(n_conv, dtype=torch.float16, device="cuda")
+    dst = torch.empty(n_conv, dtype=torch.int8, device="cuda")
+    ms = time_steps(torch, [lambda: dst.copy_(src)], 20, 4, 3)
+    res["convert_fp16_int8_gbs"] = round(3 * n_conv / (ms * 1e-3) / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    log(f"[bench] read+write ceiling (torch copies, about {nbytes} B moved): {res}")
+    return res
 
 
 # --------------------------------------------------------------------------- CPU baseline
@@ -528,18 +552,21 @@ def cpu_baseline(seconds):
     bt = rng.permutation(nb)[:n_seq * nblk].reshape(n_seq, nblk).astype(np.int32)
     q = rng.standard_normal((n_seq, h, d), dtype=np.float32).astype(np.float16)
     ref.paged_decode_attention(q, kc, vc, bt, lens, scale=1 / math.sqrt(d))   # warm-up
-    done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    calls, t0 = [], time.perf_counter()
+    while time.perf_counter() - t0 < seconds or len(calls) < 5:
+        t1 = time.perf_counter()
         ref.paged_decode_attention(q, kc, vc, bt, lens, scale=1 / math.sqrt(d))
-        done += n_seq
+        calls.append(time.perf_counter() - t1)
     dt = time.perf_counter() - t0
-    nbytes = metrics.decode_bytes([ctx] * done, h, hkv, d)
-    seq_ms = dt / done * 1e3
-    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=int(threads),
+    med = float(np.median(calls))                  # seconds per call of n_seq sequences
+    nbytes = metrics.decode_bytes([ctx] * n_seq, h, hkv, d)
+    seq_ms = med / n_seq * 1e3
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=int(threads),
                 kind="port",
-                sample=(f"numpy oracle (oracle/paged_decode_ref.py) on {done} config-2 sequences "
-                        f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32) in "
-                        f"{dt:.1f} s; {seq_ms:.2f} ms per sequence, "
+                sample=(f"numpy oracle (oracle/paged_decode_ref.py) on config-2 sequences "
+                        f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32), "
+                        f"{n_seq} per call, median of {len(calls)} calls after one warm-up "
+                        f"({dt:.1f} s); {seq_ms:.2f} ms per sequence, "
                         f"{seq_ms * 32:.1f} ms per 32-sequence step"),
                 host_cpus=os.cpu_count(), cpu_model=_cpu_model())
 
