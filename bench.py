@@ -238,23 +238,27 @@ def run_quant_write(torch, steps, warmup, seed=0):
     T = S * L
     k = torch.randn((T, hkv, d), dtype=torch.float16, device=dev, generator=gen)
     v = torch.randn((T, hkv, d), dtype=torch.float16, device=dev, generator=gen)
-    kc = torch.zeros((nb, hkv, d // 8, bs, 8), dtype=torch.int8, device=dev)
-    vc = torch.zeros((nb, hkv, d, bs), dtype=torch.int8, device=dev)
-    ks = torch.zeros((nb, hkv, bs), dtype=torch.float32, device=dev)
-    vs = torch.zeros_like(ks)
+    # Two destination caches, alternating: a step never rewrites lines that the
+    # previous step left dirty in the 256 MB Infinity Cache.
+    dests = []
+    for _ in range(2):
+        kc = torch.zeros((nb, hkv, d // 8, bs, 8), dtype=torch.int8, device=dev)
+        vc = torch.zeros((nb, hkv, d, bs), dtype=torch.int8, device=dev)
+        ks = torch.zeros((nb, hkv, bs), dtype=torch.float32, device=dev)
+        dests.append((kc, vc, ks, torch.zeros_like(ks)))
 
-    def fn():
-        pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots)
+    def mk(kc, vc, ks, vs):
+        return lambda: pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots)
 
-    ms = time_steps(torch, [fn], steps, warmup, 3)
+    ms = time_steps(torch, [mk(*dd) for dd in dests], steps, warmup, 3)
     nbytes = metrics.quant_write_bytes(T, hkv, d)
     res = dict(us=round(ms * 1e3, 2), algo_bytes=nbytes, gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
                frac_peak=round(nbytes / (ms * 1e-3) / 1e9 / metrics.MI355X_HBM_PEAK_GBS, 4),
                tokens=T, kv_heads=hkv, head_dim=d,
                slot_pattern="per-sequence block runs (prefill), block ids randomly permuted",
-               steps=steps)
+               destination_copies=len(dests), steps=steps)
     log(f"[bench] cfg3w quant_write: {res['us']} us, {res['gbs']} GB/s")
-    del k, v, kc, vc, ks, vs
+    del k, v, dests
     torch.cuda.empty_cache()
     return res
 
@@ -504,25 +508,40 @@ def read_ceiling(torch, sizes=(134_217_728, 1_073_741_824)):
 
 
 def read_write_ceiling(torch, nbytes=1 << 30):
-    """Mixed read + write rates of torch's own copy kernels (the roof the
-    write kernel shares): a same-dtype copy (1 byte read per byte written)
-    and an fp16 -> int8 conversion (2 : 1, the write kernel's ratio), each
-    moving about nbytes per step.  GB/s of bytes read plus bytes written."""
+    """Mixed read + write rates (the roof the write kernel shares), in GB/s of
+    bytes read plus bytes written: torch's same-dtype copy (1 byte read per
+    byte written, about nbytes moved) and the library's read+write probe (2
+    bytes read per byte written, the write kernel's ratio; 512 MiB read,
+    256 MiB written into one of two alternating buffers, non-temporal loads and
+    stores; best grid)."""
+    import pa_int8
+
     res = {}
     n_copy = nbytes // 2
     src = torch.ones(n_copy, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
-    ms = time_steps(torch, [lambda: dst.copy_(src)], 20, 4, 3)
+    dsts = [torch.empty_like(src) for _ in range(2)]
+    ms = time_steps(torch, [lambda dd=dd: dd.copy_(src) for dd in dsts], 20, 4, 3)
     res["copy_1to1_gbs"] = round(2 * n_copy / (ms * 1e-3) / 1e9, 1)
-    del src, dst
-    n_conv = nbytes // 3
-    src = torch.ones(n_conv, dtype=torch.float16, device="cuda")
-    dst = torch.empty(n_conv, dtype=torch.int8, device="cuda")
-    ms = time_steps(torch, [lambda: dst.copy_(src)], 20, 4, 3)
-    res["convert_fp16_int8_gbs"] = round(3 * n_conv / (ms * 1e-3) / 1e9, 1)
-    del src, dst
+    del src, dsts
+    lib = pa_int8.capi()
+    rd = 512 << 20
+    src = torch.ones(rd, dtype=torch.uint8, device="cuda")
+    # two destinations, alternating (as the write kernel's measurement)
+    dsts = [torch.empty(rd // 2, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    best = 0.0
+    for grid in (1024, 2048, 4096):
+        def mk(dst, grid=grid):
+            def f():
+                st = lib.pa_probe_read_write(src.data_ptr(), rd, dst.data_ptr(), grid,
+                                             torch.cuda.current_stream().cuda_stream)
+                assert st == 0, st
+            return f
+        ms = time_steps(torch, [mk(dd) for dd in dsts], 20, 4, 3)
+        best = max(best, (rd + rd // 2) / (ms * 1e-3) / 1e9)
+    res["probe_2to1_gbs"] = round(best, 1)
+    del src, dsts
     torch.cuda.empty_cache()
-    log(f"[bench] read+write ceiling (torch copies, about {nbytes} B moved): {res}")
+    log(f"[bench] read+write ceiling: {res}")
     return res
 
 

@@ -1,12 +1,15 @@
-// Streaming-read probes: the practical HBM read rate of the MI355X for a
-// plain contiguous sweep and for chunks in an arbitrary order (the access
-// pattern of a block-permuted paged cache).  Measurement helpers for
-// bench.py's roofline context; not part of the decode path.
+// Streaming probes: the practical HBM read rate of the MI355X for a plain
+// contiguous sweep and for chunks in an arbitrary order (the access pattern
+// of a block-permuted paged cache), and the practical rate of a contiguous
+// stream that writes one byte for every two it reads (the INT8 write
+// kernel's ratio).  Measurement helpers for bench.py's roofline context; not
+// part of the decode path.
 //
-// Both probes keep several independent 16-byte loads per lane in flight and
-// fold every loaded word into a checksum, so the compiler can neither narrow
-// nor drop a load.  They load with the non-temporal hint, as the decode
-// kernels do.
+// The read probes keep several independent 16-byte loads per lane in flight
+// and fold every loaded word into a checksum, so the compiler can neither
+// narrow nor drop a load.  They load with the non-temporal hint, as the
+// decode kernels' V loads do; the read+write probe also stores with the
+// write kernel's non-temporal policy.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -79,6 +82,35 @@ probe_read_chunks(const uint4* __restrict__ p, const int32_t* __restrict__ order
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// Reads 16 B and writes 8 B (a fold of them) per lane and element, 4
+// elements per lane in flight: the read and written streams are contiguous.
+__global__ void __launch_bounds__(kProbeThreads)
+probe_read_write(const uint4* __restrict__ p, size_t n16, void* dst) {
+  const auto out = __builtin_amdgcn_make_buffer_rsrc(dst, 0, (int)(uint32_t)(n16 * 8), 0x00020000);
+  const size_t step = (size_t)gridDim.x * kProbeThreads * kUnroll;
+  size_t i = (size_t)blockIdx.x * kProbeThreads * kUnroll + threadIdx.x;
+  typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
+  constexpr int kStorePolicy = 2;   // non-temporal, as the write kernel's tile stores
+  for (; i + (kUnroll - 1) * kProbeThreads < n16; i += step) {
+    uint4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = ld(p + i + u * kProbeThreads);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      __builtin_amdgcn_raw_buffer_store_b64((u2v_t){v[u].x ^ v[u].z, v[u].y ^ v[u].w}, out,
+                                            (uint32_t)((i + u * kProbeThreads) * 8), 0,
+                                            kStorePolicy);
+  }
+  for (int u = 0; u < kUnroll; ++u) {   // ragged end of the sweep
+    const size_t e = i + u * kProbeThreads;
+    if (e < n16) {
+      const uint4 w = ld(p + e);
+      __builtin_amdgcn_raw_buffer_store_b64((u2v_t){w.x ^ w.z, w.y ^ w.w}, out, (uint32_t)(e * 8),
+                                            0, kStorePolicy);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -104,6 +136,18 @@ pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* o
   if (total > (size_t)INT32_MAX) return PA_ERR_BAD_SHAPE;
   probe_read_chunks<<<grid, kProbeThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<const uint4*>(src), order, num_chunks, (int32_t)total, chunk_bytes / 16, sink);
+  return hipGetLastError() == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+}
+
+pa_status_t pa_probe_read_write(const void* src, size_t read_bytes, void* dst, int32_t grid,
+                               pa_stream_t stream) {
+  if (!src || !dst) return PA_ERR_NULL_POINTER;
+  const size_t n16 = read_bytes / 16;
+  if (grid < 1 || reinterpret_cast<uintptr_t>(src) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(dst) % 8 != 0 || n16 * 8 > 0xFFFFFFFFull)
+    return PA_ERR_BAD_SHAPE;
+  probe_read_write<<<grid, kProbeThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint4*>(src), n16, dst);
   return hipGetLastError() == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
 

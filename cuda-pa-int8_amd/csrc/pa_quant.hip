@@ -137,12 +137,14 @@ __device__ __forceinline__ uint2 quant_group_exact(uint4 xv, float s) {
                     b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
 }
 
-// Cache policy of the cache-tile stores (buffer store aux bits): sc1, the
-// write-through policy.  With the inputs read non-temporally it took the
-// config-3 write (524,288 tokens x 2 heads) from 169 to 156 us on MI355X: the
-// written tiles leave the L2 at once instead of as later write-backs between
-// the input reads.
-constexpr int kTileStorePolicy = 16;
+// Cache policy of the cache-tile stores (buffer store aux bits): nt, the
+// streaming policy; the tiles are not read again by this kernel.  Measured on
+// MI355X on the config-3 write (524,288 tokens x 2 heads, inputs read
+// non-temporally) with two destination caches in turn, so that no call
+// rewrites lines the previous call left in the Infinity Cache: nt 166-167 us,
+// sc1 (write-through) 170 us, no hint 178 us.  (Rewriting one destination
+// favours sc1 and plain stores, whose lines that cache absorbs: 158 us.)
+constexpr int kTileStorePolicy = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);

@@ -81,6 +81,7 @@ PROTOTYPES = {
                                                 _i32, _p, _p, _i32, _i32, _i32, _p]),
     "pa_probe_read_contiguous": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
     "pa_probe_read_chunks": (ctypes.c_int, [_p, _sz, _p, _i32, _i32, _p, _i32, _p]),
+    "pa_probe_read_write": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
 }
 
 

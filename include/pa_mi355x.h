@@ -227,8 +227,8 @@ pa_status_t pa_reshape_and_cache_f16(
     void* k_cache, void* v_cache, int32_t num_blocks, int32_t block_size, int32_t x,
     pa_stream_t stream);
 
-/* Measurement helpers (no reference counterpart): streaming-read probes that
- * give bench.py the practical HBM read rate next to the decode numbers.
+/* Measurement helpers (no reference counterpart): streaming probes that give
+ * bench.py the practical HBM rates next to the decode and write numbers.
  * pa_probe_read_contiguous sweeps `bytes` from `src` with 16-byte loads;
  * pa_probe_read_chunks reads `num_chunks` chunks of `chunk_bytes` (1024,
  * 2048 or a multiple of 4096) at src + order[i] * chunk_bytes, skipping order
@@ -239,6 +239,11 @@ pa_status_t pa_probe_read_contiguous(const void* src, size_t bytes, uint32_t* si
 pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* order,
                                  int32_t num_chunks, int32_t chunk_bytes, uint32_t* sink,
                                  int32_t grid, pa_stream_t stream);
+/* pa_probe_read_write reads `read_bytes` (a multiple of 16) from `src` and
+ * writes read_bytes / 2 to `dst` (below 4 GiB), both contiguous: the
+ * practical rate of a stream with the INT8 write kernel's read : write ratio. */
+pa_status_t pa_probe_read_write(const void* src, size_t read_bytes, void* dst, int32_t grid,
+                                pa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -122,6 +122,9 @@ def test_probe_host_checks(lib):
         assert lib.pa_probe_read_chunks(16, 1 << 20, 16, 4, chunk, 16, 64, None) == 2
     assert lib.pa_probe_read_chunks(None, 1 << 20, 16, 4, 4096, 16, 64, None) == 1
     assert lib.pa_probe_read_contiguous(16, 1 << 20, 16, 0, None) == 2
+    assert lib.pa_probe_read_write(None, 1 << 20, 16, 64, None) == 1
+    assert lib.pa_probe_read_write(16, 1 << 20, 16, 0, None) == 2
+    assert lib.pa_probe_read_write(16, 1 << 34, 16, 64, None) == 2     # output past 4 GiB
 
 
 def test_waves_override_hook(lib):
