@@ -108,8 +108,10 @@ def make_case(torch, lens, num_heads, num_kv_heads, head_dim, bs, dev, seed, int
 
 
 def copies_for(bytes_per_copy):
-    """Enough distinct cache copies that the rotation outruns the Infinity Cache."""
-    return max(1, min(8, math.ceil(2 * MALL_BYTES / max(1, bytes_per_copy))))
+    """Enough distinct cache copies that the rotation outruns the Infinity Cache:
+    at least 4x its size in total (the V tiles are read non-temporally, so the
+    lines that can stay in it are K's, half of each copy)."""
+    return max(1, min(8, math.ceil(4 * MALL_BYTES / max(1, bytes_per_copy))))
 
 
 # --------------------------------------------------------------------------- timing
