@@ -878,7 +878,8 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
 // and claims the next one from the class counter once the current item's
 // first loads are issued.  Exactly as many claims as the class has items are
 // made per launch, so the claim that returns the last index is the last one
-// and resets the counter for the next launch.  No work-group is launched for
+// and resets the counter for the next launch; a class with no more items than
+// work-groups makes none.  No work-group is launched for
 // a split that a sequence does not have, whatever the block-table capacity or
 // the spread of the lengths.
 struct SchedArgs {
@@ -1089,11 +1090,15 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
   // Item indices are compared unsigned: whatever a claim counter holds, no
   // work-group leaves its class's item list.
   int idx = blockIdx.x >> 3;   // index within the class: static first item
+  // With no more items than work-groups in the class (equal lengths give one
+  // item per work-group) the static first items cover the class: no claims,
+  // and the counter stays at zero.
+  const bool claims = items_c > groups_c;
   while ((uint32_t)idx < (uint32_t)items_c) {
     // The next item is claimed once this item's first loads are out.
     uint32_t old = 0;
     auto claim = [&] {
-      if (threadIdx.x == 0)
+      if (claims && threadIdx.x == 0)
         old = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     const int row = cls + 8 * (idx / per_row);
@@ -1124,6 +1129,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
     // the last one and resets the counter for the next launch.
+    if (!claims) break;
     if (threadIdx.x == 0) {
       if (old == (uint32_t)(items_c - 1))
         __hip_atomic_store(queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
