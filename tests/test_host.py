@@ -268,3 +268,22 @@ def test_bench_dense_gather_inverts_the_paged_layout():
     want_k = np.repeat(k.transpose(0, 2, 1, 3), h // hkv, axis=1)
     want_v = np.repeat(v.transpose(0, 2, 1, 3), h // hkv, axis=1)
     assert np.array_equal(kd.numpy(), want_k) and np.array_equal(vd.numpy(), want_v)
+
+
+def test_bench_rotation_outruns_the_infinity_cache():
+    """Decode caches rotate over at least 4x the 256 MB Infinity Cache (2x let
+    K lines hit in it on MI355X) unless the 8-copy cap binds, which only
+    happens for caches far smaller than it (launch-bound configs)."""
+    import sys
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+
+    mall = 256 << 20
+    for nbytes in (4_203_024, 134_447_232, 277_348_608, 537_395_456, 553_844_768,
+                   1_073_938_464, 4_295_360_544):
+        n = bench.copies_for(nbytes)
+        assert 1 <= n <= 8
+        assert n * nbytes >= 4 * mall or n == 8, (nbytes, n)
+    assert bench.copies_for(134_447_232) == 8          # config 2: 1.08 GB cycled
+    assert bench.copies_for(537_395_456) == 2          # config 3 FP16: 1.07 GB
