@@ -26,6 +26,7 @@ std::atomic<int> g_waves_override{0};
 std::atomic<int> g_schedule_mode{0};   // 0 auto, 1 grid, 2 in-kernel schedule
 std::atomic<int> g_load_mode{0};       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
 constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
+constexpr int kKntMinPartition = 4096;          // non-temporal K rows from this split size
 // Upper bound on resident decode work-groups used to size the partial
 // buffers of the in-kernel schedule (256 CUs x 2 groups on MI355X).
 constexpr int kSchedGroupsBound = 1024;
@@ -61,7 +62,8 @@ struct Plan {
   int rows_max = 0;
   int pmin = 0, pmax = 0;
   int pmin_uniform = 0;   // lower bound the kernel uses when all lengths are equal
-  bool nt_loads = false;  // non-temporal cache-tile loads
+  bool nt_loads = false;  // non-temporal V-row loads
+  bool k_nt = false;      // non-temporal K-row loads too
 };
 
 Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_heads,
@@ -104,9 +106,9 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   p.nsplit = (int)((ctx + part - 1) / part);
 
   // V-row loads: non-temporal when every K/V byte is read by exactly one
-  // work-group (one head chunk per kv head); MI355X streams them faster (FP16
-  // config 3: 94 -> 84 us, config 4 32k: 184 -> 166 us, when K took the same
-  // policy; K rows now always load plain, see load_tile).  With several head
+  // work-group (one head chunk per kv head); MI355X streams them faster (plain
+  // V: config 3 FP16 +10%, INT8 +6%; K rows, see load_tile and k_nt below,
+  // follow their own rule).  With several head
   // chunks per kv head the chunks find the tiles in the L2 only with plain
   // loads (MQA 32/1 of config 5: 71 us plain, 95 us non-temporal).
   // A launch that reads little (bound: every sequence at `ctx` tokens) is
@@ -125,6 +127,11 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   const int mode = g_schedule_mode.load(std::memory_order_relaxed);
   p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
   if (num_seqs > pa::kSchedMaxSeqs) p.sched = false;
+  // K rows non-temporal as well: FP16 grid launches whose splits hold at least
+  // kKntMinPartition tokens (same box, caches rotated over 4x the Infinity
+  // Cache: config 3 FP16 89.6 -> 86.4 us; config 2's 1024-token splits and
+  // INT8 measured faster with plain K).
+  p.k_nt = p.nt_loads && is_f16(kind) && !p.sched && p.partition >= kKntMinPartition;
   if (p.sched) {
     if (partition_tokens > 0) {
       p.pmin = p.pmax = p.pmin_uniform = p.partition;
@@ -231,6 +238,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.int8_kv = !is_f16(kind);
   l.fused = is_fused(kind);
   l.nt_loads = p.nt_loads;
+  l.k_nt = p.k_nt;
   l.stream = reinterpret_cast<hipStream_t>(stream);
   pa::DecodeShape& sh = l.shape;
   sh.num_seqs = num_seqs;

@@ -81,12 +81,15 @@ __device__ __forceinline__ float head_sum(float v) {
 
 // Loads of cache tiles.  NTL: non-temporal, for tiles that no other
 // work-group of the launch reads (one head chunk per kv head); otherwise plain,
-// so the head chunks that share a kv head find its tiles in the L2.  Only V
-// rows take the non-temporal form: a V load instruction covers whole 128-B
-// lines, while each K line is read half by one instruction and half by the
-// next (the two token halves of a row group), and non-temporal K lines left
-// the L2 in between (INT8 config 3 fetched 7% more; plain K loads measured
-// 11% faster for INT8 and 6-7% for FP16).
+// so the head chunks that share a kv head find its tiles in the L2.  V rows
+// take the non-temporal form under NTL: a V load instruction covers whole
+// 128-B lines.  Each K line is read half by one instruction and half by the
+// next (the two token halves of a row group), and non-temporal K lines can
+// leave the L2 in between (INT8 config 3 fetched 7% more), so K rows load
+// plain except under KNT, which the planner sets for FP16 grid launches with
+// long splits (>= 4096 tokens), where non-temporal K measured faster
+// (config 3 FP16 3.6%; plain K stays ahead for INT8, ragged batches and
+// shorter splits).
 template <typename T, bool NTL>
 __device__ __forceinline__ T load_tile(const void* p) {
   if constexpr (NTL) return load_stream<T>(p);
@@ -245,8 +248,8 @@ struct SplitWork {
 // `resolve(ctx, ns)` supplies the context length and split count once the
 // split's block-id loads are in flight (the grid kernel reads them from
 // memory then) and returns false when the split holds no tokens.
-template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, bool NTL, typename Resolve,
-          typename AfterIssue>
+template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, bool NTL, bool KNT,
+          typename Resolve, typename AfterIssue>
 __device__ __forceinline__ void decode_split(
     const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
     const float* __restrict__ ksc, const float* __restrict__ vsc, const int* __restrict__ bt,
@@ -410,7 +413,7 @@ __device__ __forceinline__ void decode_split(
       for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk)
-          kw[p][kk] = load_tile<uint4, false>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
+          kw[p][kk] = load_tile<uint4, KNT>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
       return;
     }
 #pragma unroll
@@ -423,8 +426,8 @@ __device__ __forceinline__ void decode_split(
 #pragma unroll
       for (int kk = 0; kk < KC; ++kk) {
         const uint8_t* p0 = kp + (size_t)(4 * kk) * bs * 8 * ESZ;
-        kx[p][kk] = load_tile<LVec, false>(p0);
-        ky[p][kk] = load_tile<LVec, false>(p0 + 4 * 8 * ESZ);
+        kx[p][kk] = load_tile<LVec, KNT>(p0);
+        ky[p][kk] = load_tile<LVec, KNT>(p0 + 4 * 8 * ESZ);
       }
     }
   };
@@ -799,7 +802,7 @@ __device__ __forceinline__ void decode_split(
   sh.num_blocks = sh_num_blocks
 
 // Grid form: one work-group per (unit, split) slot of the host's plan.
-template <int D, int NW, bool I8, bool FUSED, bool NTL>
+template <int D, int NW, bool I8, bool FUSED, bool NTL, bool KNT>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE_HEAD_PARAMS,
               DecodeShape sh_tail, const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
@@ -858,7 +861,7 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
     return split < ns;
   };
-  decode_split<D, NW, I8, FUSED, false, NTL>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
+  decode_split<D, NW, I8, FUSED, false, NTL, KNT>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
                                              sm, resolve, [] {});
 }
 
@@ -1127,7 +1130,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                                  : split * P + __builtin_amdgcn_readfirstlane((int)ss.rem[seq]);
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
-    decode_split<D, NW, I8, FUSED, true, NTL>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
+    decode_split<D, NW, I8, FUSED, true, NTL, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
                                               wk, sm, [](int&, int&) { return true; }, claim);
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
@@ -1195,6 +1198,30 @@ splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ p
                                    ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
 }
 
+template <int D, int NW, bool I8, bool NTL, bool KNT>
+hipError_t launch_decode_grid(const DecodeLaunch& l, int grid) {
+  const DecodeShape& sh = l.shape;
+  const auto* q = static_cast<const half_t*>(l.q);
+  const auto* kc = static_cast<const uint8_t*>(l.k_cache);
+  const auto* vc = static_cast<const uint8_t*>(l.v_cache);
+  auto* out = static_cast<half_t*>(l.out);
+  if (l.fused) {
+    decode_kernel<D, NW, I8, true, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
+        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+        l.part_ml, l.counters);
+    return hipGetLastError();
+  }
+  decode_kernel<D, NW, I8, false, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
+      l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
+      l.part_ml, l.counters);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
+  splitk_reduce_kernel<D><<<units, kThreads, 0, l.stream>>>(l.part_acc, l.part_ml, l.context_lens,
+                                                            out, sh);
+  return hipGetLastError();
+}
+
 template <int D, int NW, bool I8, bool NTL>
 hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const DecodeShape& sh = l.shape;
@@ -1225,25 +1252,10 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const int grid = sh.num_items >= 8
                        ? (sh.num_items + 7) / 8 * 8 * sh.num_kv_heads * sh.nchunk
                        : (sh.num_items * sh.num_kv_heads + 7) / 8 * 8 * sh.nchunk;
-  const auto* q = static_cast<const half_t*>(l.q);
-  const auto* kc = static_cast<const uint8_t*>(l.k_cache);
-  const auto* vc = static_cast<const uint8_t*>(l.v_cache);
-  auto* out = static_cast<half_t*>(l.out);
-  if (l.fused) {
-    decode_kernel<D, NW, I8, true, NTL><<<grid, NW * kWave, 0, l.stream>>>(
-        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
-        l.part_ml, l.counters);
-    return hipGetLastError();
+  if constexpr (!I8 && NTL) {
+    if (l.k_nt) return launch_decode_grid<D, NW, I8, NTL, true>(l, grid);
   }
-  decode_kernel<D, NW, I8, false, NTL><<<grid, NW * kWave, 0, l.stream>>>(
-      l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
-      l.part_ml, l.counters);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
-  splitk_reduce_kernel<D><<<units, kThreads, 0, l.stream>>>(l.part_acc, l.part_ml, l.context_lens,
-                                                            out, sh);
-  return hipGetLastError();
+  return launch_decode_grid<D, NW, I8, NTL, false>(l, grid);
 }
 
 template <int D, bool I8, bool NTL>

@@ -64,7 +64,8 @@ struct DecodeLaunch {
   int waves;           // waves per decode work-group: 4 or 8 (head_dim <= 128)
   bool int8_kv;
   bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
-  bool nt_loads;       // non-temporal cache-tile loads (one head chunk per kv head)
+  bool nt_loads;       // non-temporal V-row loads (one head chunk per kv head)
+  bool k_nt;           // non-temporal K-row loads too (FP16 grid launches, long splits)
   DecodeShape shape;
   // In-kernel schedule (sched = true): `groups` resident work-groups claim
   // (row, kv head) items; the partials hold `rows_max` slot rows.

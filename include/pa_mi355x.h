@@ -125,9 +125,10 @@ pa_status_t pa_decode_set_waves_per_group(int32_t waves);
 pa_status_t pa_decode_set_schedule(int32_t mode);
 
 /* Tuning hook (no reference counterpart): how later decode calls in this
- * process load V cache rows (K rows always use plain loads: each K line is
- * read by two consecutive load instructions and must stay in the L2 between
- * them).  0 = automatic: non-temporal loads when each
+ * process load V cache rows.  (K rows use plain loads, since each K line is
+ * read by two consecutive load instructions, except in FP16 grid launches
+ * whose splits hold at least 4096 tokens, which load K non-temporally too
+ * whenever V is.)  0 = automatic: non-temporal loads when each
  * kv head's tiles are read by one work-group (query heads per kv head <= 16)
  * and the call reads more than 32 MB of K/V; plain loads when several head
  * chunks share the tiles through the L2, or when a small cache may still sit
