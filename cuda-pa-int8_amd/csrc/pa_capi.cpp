@@ -107,10 +107,10 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
 
   // V-row loads: non-temporal when every K/V byte is read by exactly one
   // work-group (one head chunk per kv head); MI355X streams them faster (plain
-  // V: config 3 FP16 +10%, INT8 +6%; K rows, see load_tile and k_nt below,
-  // follow their own rule).  With several head
-  // chunks per kv head the chunks find the tiles in the L2 only with plain
-  // loads (MQA 32/1 of config 5: 71 us plain, 95 us non-temporal).
+  // V: config 3 FP16 +10%, INT8 +6%; K rows follow their own rule, see
+  // load_tile and k_nt below).  With several head chunks per kv head the
+  // chunks find the tiles in the L2 only with plain loads (MQA 32/1 of
+  // config 5: 71 us plain, 95 us non-temporal).
   // A launch that reads little (bound: every sequence at `ctx` tokens) is
   // latency-bound and its tiles may still sit in the 256 MB Infinity Cache
   // from an earlier call, which plain loads can hit (config 1: 4.6 us plain,
