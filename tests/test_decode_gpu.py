@@ -464,3 +464,28 @@ def test_graph_replay_matches_eager(variant):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_load_policies_agree(head_dim, policy):
+    """Every cache-load hint gives the oracle's result: plain (1), non-temporal
+    V (2; FP16 grid launches with splits of >= 4096 tokens then load K
+    non-temporally too) and automatic (0), on the grid and the scheduled forms,
+    with two splits of 4096 tokens per sequence."""
+    import pa_int8
+
+    lib = pa_int8.capi()
+    lens = np.array([8192, 5000], np.int32)
+    c = fp16_case(2, lens, 8, 2, head_dim=head_dim, seed=40 + policy)
+    want = oracle_fp16(c)
+    try:
+        assert lib.pa_decode_set_load_policy(policy) == 0
+        for mode in (0, 1):
+            assert lib.pa_decode_set_schedule(mode) == 0
+            for variant in F16_VARIANTS:
+                assert_close(run_fp16(c, variant, partition=4096), want,
+                             what=f"{variant} D={head_dim} policy={policy} schedule={mode}")
+    finally:
+        lib.pa_decode_set_load_policy(0)
+        lib.pa_decode_set_schedule(0)
