@@ -624,7 +624,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              f"(the decode path runs on a single MI355X; see DESIGN.md for how it would shard)",
+              f"(the decode path runs on a single MI355X; it would shard by sequence or kv head, "
+              f"with no communication)",
               file=sys.stderr)
         sys.exit(2)
 
