@@ -466,13 +466,13 @@ def run_configs(torch, names, steps, warmup):
 # --------------------------------------------------------------------------- ceiling probes
 
 def read_ceiling(torch, sizes=(134_217_728, 1_073_741_824)):
-    """Practical HBM read rates from the library's streaming-read probes: a
+    """Practical HBM read rates from the benchmark's streaming-read probes: a
     contiguous sweep and chunks in random order -- 4 KB (one FP16 K or V tile
     of a block, D=128) and 2 KB (one INT8 tile) -- at the headline's size and
     at 1 GiB; best grid of a few, MALL-rotated."""
-    import pa_int8
+    from pa_int8._loader import probe_capi
 
-    lib = pa_int8.capi()
+    lib = probe_capi()
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     out = {}
     for nbytes in sizes:
@@ -516,7 +516,7 @@ def read_write_ceiling(torch, nbytes=1 << 30):
     bytes read per byte written, the write kernel's ratio; 512 MiB read,
     256 MiB written into one of two alternating buffers, non-temporal loads and
     stores; best grid)."""
-    import pa_int8
+    from pa_int8._loader import probe_capi
 
     res = {}
     n_copy = nbytes // 2
@@ -525,7 +525,7 @@ def read_write_ceiling(torch, nbytes=1 << 30):
     ms = time_steps(torch, [lambda dd=dd: dd.copy_(src) for dd in dsts], 20, 4, 3)
     res["copy_1to1_gbs"] = round(2 * n_copy / (ms * 1e-3) / 1e9, 1)
     del src, dsts
-    lib = pa_int8.capi()
+    lib = probe_capi()
     rd = 512 << 20
     src = torch.ones(rd, dtype=torch.uint8, device="cuda")
     # two destinations, alternating (as the write kernel's measurement)

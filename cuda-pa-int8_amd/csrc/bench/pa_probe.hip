@@ -2,8 +2,9 @@
 // contiguous sweep and for chunks in an arbitrary order (the access pattern
 // of a block-permuted paged cache), and the practical rate of a contiguous
 // stream that writes one byte for every two it reads (the INT8 write
-// kernel's ratio).  Measurement helpers for bench.py's roofline context; not
-// part of the decode path.
+// kernel's ratio).  Measurement helpers for bench.py's roofline context,
+// built into their own library (libpa_bench_probe.so, declared in
+// pa_probe.h); not part of the decode path or its C ABI.
 //
 // The read probes keep several independent 16-byte loads per lane in flight
 // and fold every loaded word into a checksum, so the compiler can neither
@@ -14,7 +15,7 @@
 #include <stdint.h>
 
 #include "pa_device.hpp"
-#include "pa_mi355x.h"
+#include "pa_probe.h"
 
 namespace {
 

@@ -31,7 +31,11 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
                        const int64_t* __restrict__ slots, int num_tokens, int num_kv_heads,
                        half_t* __restrict__ kc, half_t* __restrict__ vc, int num_blocks, int bs,
                        int bs_log2, int njobs) {
-  constexpr int JQ = D / 32;   // 16-B groups per lane
+  static_assert(D % 16 == 0, "head_dim must be a multiple of 16");
+  constexpr int DG = D / 8;            // 8-dim groups of a row
+  constexpr int JQ = (DG + 3) / 4;     // 16-B groups per lane: dim groups (l >> 4) + 4j
+  // (with head_dim % 32 == 16 the last j is a group only for lanes l >> 4 < 2;
+  // the others load the row's last group, in bounds, and store nothing)
   __shared__ __attribute__((aligned(16))) half_t tile[kWriteWaves][D * 16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -52,7 +56,8 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
                              : key + (int64_t)tc * kts + (int64_t)h * khs;
     uint4 x[JQ];
 #pragma unroll
-    for (int j = 0; j < JQ; ++j) x[j] = *reinterpret_cast<const uint4*>(src + (qq + 4 * j) * 8);
+    for (int j = 0; j < JQ; ++j)
+      x[j] = *reinterpret_cast<const uint4*>(src + (qq + 4 * j < DG ? qq + 4 * j : DG - 1) * 8);
     const int64_t slot = tv ? slots[tc] : -1;
     const bool sok = slot >= 0 && slot < pool;
     // block_size is a power of two: shifts instead of a 64-bit division
@@ -64,7 +69,7 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
 #pragma unroll
       for (int j = 0; j < JQ; ++j) {
         const int o = qq + 4 * j;
-        if (sok) *reinterpret_cast<uint4*>(kc + ((bh * (D / 8) + o) * bs + off) * 8) = x[j];
+        if (sok && o < DG) *reinterpret_cast<uint4*>(kc + ((bh * DG + o) * bs + off) * 8) = x[j];
       }
       continue;
     }
@@ -79,6 +84,7 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
 #pragma unroll
       for (int j = 0; j < JQ; ++j) {
         const int o = qq + 4 * j;
+        if (o >= DG) continue;
         const uint32_t wv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -107,6 +113,7 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
 #pragma unroll
       for (int j = 0; j < JQ; ++j) {
         const int o = qq + 4 * j;
+        if (o >= DG) continue;
         const uint32_t wv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -138,9 +145,10 @@ static hipError_t launch_write_d(const CacheWriteLaunch& l) {
 
 hipError_t launch_cache_write_f16(const CacheWriteLaunch& l) {
   switch (l.head_dim) {
-    case 64: return launch_write_d<64>(l);
-    case 128: return launch_write_d<128>(l);
-    case 256: return launch_write_d<256>(l);
+#define PA_CASE(D) \
+  case D: return launch_write_d<D>(l);
+    PA_FOR_EACH_HEAD_DIM(PA_CASE)
+#undef PA_CASE
     default: return hipErrorInvalidValue;
   }
 }

@@ -3,14 +3,41 @@
 // Host side only: argument validation (the reference's TORCH_CHECKs made
 // device-free), split planning, workspace carving and kernel dispatch.
 #include "pa_mi355x.h"
+#include "pa_mi355x_tuning.h"
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <atomic>
 #include <cstdint>
 
 #include "pa_internal.hpp"
+
+namespace pa {
+namespace {
+
+// Dispatch on head_dim to the per-head_dim instantiations.
+hipError_t launch_decode(const DecodeLaunch& l) {
+  switch (l.head_dim) {
+#define PA_CASE(D) \
+  case D: return launch_decode_d##D(l);
+    PA_FOR_EACH_HEAD_DIM(PA_CASE)
+#undef PA_CASE
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int sched_groups(int head_dim, int waves, bool int8_kv) {
+  switch (head_dim) {
+#define PA_CASE(D) \
+  case D: return sched_groups_d##D(waves, int8_kv);
+    PA_FOR_EACH_HEAD_DIM(PA_CASE)
+#undef PA_CASE
+    default: return 0;
+  }
+}
+
+}  // namespace
+}  // namespace pa
 
 namespace {
 
@@ -22,9 +49,10 @@ constexpr int kRefTile = 128;        // reference TILE (paged_attention_v3_warp.
 constexpr int kTargetWaves = 2048;   // waves one decode launch aims for (256 CUs x 8)
 constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
 constexpr int kSchedMinPartition = 1024;   // per 4 waves, in-kernel schedule
-std::atomic<int> g_waves_override{0};
-std::atomic<int> g_schedule_mode{0};   // 0 auto, 1 grid, 2 in-kernel schedule
-std::atomic<int> g_load_mode{0};       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
+// Test and tuning overrides (pa_mi355x_tuning.h), per calling thread.
+thread_local int g_waves_override = 0;
+thread_local int g_schedule_mode = 0;   // 0 auto, 1 grid, 2 in-kernel schedule
+thread_local int g_load_mode = 0;       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
 constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
 constexpr int kKntMinPartition = 4096;          // non-temporal K rows from this split size
 // Upper bound on resident decode work-groups used to size the partial
@@ -34,7 +62,15 @@ constexpr size_t kAlign = 256;
 
 bool is_f16(pa_decode_kind_t k) { return k == PA_DECODE_WARP_F16 || k == PA_DECODE_SPLITK_F16; }
 bool is_fused(pa_decode_kind_t k) { return k == PA_DECODE_WARP_F16 || k == PA_DECODE_WARP_I8; }
-bool supported_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
+bool supported_head_dim(int d) {
+  switch (d) {
+#define PA_CASE(D) case D:
+    PA_FOR_EACH_HEAD_DIM(PA_CASE)
+#undef PA_CASE
+    return true;
+    default: return false;
+  }
+}
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 int ilog2(int v) {
   int r = 0;
@@ -74,7 +110,7 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   p.head_tile = head_tile_for(group);
   p.nchunk = group / p.head_tile;
   p.units = num_seqs * num_kv_heads * p.nchunk;
-  const int ov = g_waves_override.load(std::memory_order_relaxed);
+  const int ov = g_waves_override;
   p.waves = (ov == 4 || ov == 8) ? ov : 8;
   // Split-K kinds with INT8 KV or with several head chunks per kv head: two
   // 4-wave work-groups per CU, so that one group's item start (block ids, then
@@ -117,14 +153,14 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // 6.0 us non-temporal); non-temporal loads start at 32 MB.
   const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
                              (is_f16(kind) ? 2 : 1);
-  const int lm = g_load_mode.load(std::memory_order_relaxed);
+  const int lm = g_load_mode;
   p.nt_loads = lm == 2 || (lm == 0 && p.nchunk == 1 && kv_bytes > kNtMinBytes);
 
   // Work distribution.  The split-K kinds (long and ragged contexts) use the
   // in-kernel schedule: no empty work-groups and largest-first items (config
   // 5 of the bench: 10-37% faster than the grid).  The single-launch kinds
   // keep the grid, which saves the schedule's start-up for equal lengths.
-  const int mode = g_schedule_mode.load(std::memory_order_relaxed);
+  const int mode = g_schedule_mode;
   p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
   if (num_seqs > pa::kSchedMaxSeqs) p.sched = false;
   // K rows non-temporal as well: FP16 grid launches whose splits hold at least
@@ -154,27 +190,31 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   return p;
 }
 
-// Workspace: [arrival counters | claim counter] (zero between calls), then the
-// schedule info (in-kernel schedule only), then the split partials.
-struct WsLayout {
-  size_t counters = 0, info = 0, ml = 0, acc = 0, total = 0;
-};
-
-// Arrival counters, then the 8 claim counters of the in-kernel schedule.
+// Counters (zero between calls): the 8 claim counters of the in-kernel
+// schedule at a fixed offset, then one arrival counter per unit.  Workspace
+// (scratch): the schedule record (in-kernel schedule only), then the split
+// partials.
 constexpr size_t kQueueBytes = 8 * pa::kSchedQueueStride * sizeof(uint32_t);
 size_t counter_region(int units) {
-  return align_up((size_t)units * sizeof(uint32_t)) + align_up(kQueueBytes);
+  return align_up(kQueueBytes) + align_up((size_t)units * sizeof(uint32_t));
+}
+
+struct WsLayout {
+  size_t info = 0, ml = 0, acc = 0, total = 0;
+};
+
+size_t slot_count(const Plan& p, int num_seqs) {
+  return p.sched ? (size_t)p.rows_max * p.units / std::max(1, num_seqs)
+                 : (size_t)p.units * p.nsplit;
 }
 
 WsLayout ws_layout(const Plan& p, int head_dim, int num_seqs) {
   WsLayout w;
-  w.counters = counter_region(p.units);
-  const size_t slots = p.sched ? (size_t)p.rows_max * p.units / std::max(1, num_seqs)
-                               : (size_t)p.units * p.nsplit;
+  const size_t slots = slot_count(p, num_seqs);
   w.info = p.sched ? align_up((size_t)(1 + num_seqs) * sizeof(int)) : 0;
   w.ml = align_up(slots * p.head_tile * 2 * sizeof(float));
   w.acc = align_up(slots * p.head_tile * head_dim * sizeof(float));
-  w.total = w.counters + w.info + w.ml + w.acc;
+  w.total = w.info + w.ml + w.acc;
   return w;
 }
 
@@ -184,7 +224,8 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
                           int32_t block_size, int32_t num_seqs, int32_t num_heads,
                           int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks, int32_t x,
                           int32_t max_blocks, int32_t max_context_len, int32_t partition_tokens,
-                          void* workspace, size_t workspace_bytes, pa_stream_t stream) {
+                          void* counters, size_t counter_bytes, void* workspace,
+                          size_t workspace_bytes, pa_stream_t stream) {
   pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads,
                                       num_blocks, block_size, x, max_blocks);
   if (st != PA_OK) return st;
@@ -202,8 +243,11 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
     if (groups * p.waves * 64 > 0xFFFFFFFFll) return PA_ERR_BAD_SHAPE;
   }
   const WsLayout wl = ws_layout(p, head_dim, num_seqs);
+  if (!counters || counter_bytes < counter_region(p.units)) return PA_ERR_WORKSPACE;
   if (!workspace || workspace_bytes < wl.total) return PA_ERR_WORKSPACE;
-  if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0) return PA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0 ||
+      reinterpret_cast<uintptr_t>(counters) % kAlign != 0)
+    return PA_ERR_WORKSPACE;
 
   pa::DecodeLaunch l{};
   l.out = out;
@@ -214,12 +258,13 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.v_scales = v_scales;
   l.block_table = block_table;
   l.context_lens = context_lens;
+  char* cn = static_cast<char*>(counters);
+  l.queue = reinterpret_cast<uint32_t*>(cn);
+  l.counters = reinterpret_cast<uint32_t*>(cn + align_up(kQueueBytes));
   char* ws = static_cast<char*>(workspace);
-  l.counters = reinterpret_cast<uint32_t*>(ws);
-  l.queue = reinterpret_cast<uint32_t*>(ws + wl.counters - align_up(kQueueBytes));
-  l.sched_info = reinterpret_cast<int*>(ws + wl.counters);
-  l.part_ml = reinterpret_cast<float*>(ws + wl.counters + wl.info);
-  l.part_acc = reinterpret_cast<float*>(ws + wl.counters + wl.info + wl.ml);
+  l.sched_info = reinterpret_cast<int*>(ws);
+  l.part_ml = reinterpret_cast<float*>(ws + wl.info);
+  l.part_acc = reinterpret_cast<float*>(ws + wl.info + wl.ml);
   l.sched = p.sched;
   l.rows_max = p.rows_max;
   l.pmin = p.pmin;
@@ -227,9 +272,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   l.pmax = p.pmax;
   if (p.sched) {
     const bool i8 = !is_f16(kind);
-    l.groups = head_dim == 64    ? pa::sched_groups_d64(p.waves, i8)
-               : head_dim == 128 ? pa::sched_groups_d128(p.waves, i8)
-                                 : pa::sched_groups_d256(p.waves, i8);
+    l.groups = pa::sched_groups(head_dim, p.waves, i8);
     if (l.groups <= 0) return PA_ERR_LAUNCH;
     l.groups = std::min(l.groups, kSchedGroupsBound);
   }
@@ -256,13 +299,7 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   sh.num_items = num_seqs * p.nsplit;
   sh.scale_log2 = scale * 1.4426950408889634f;
 
-  hipError_t e;
-  switch (head_dim) {
-    case 64: e = pa::launch_decode_d64(l); break;
-    case 128: e = pa::launch_decode_d128(l); break;
-    default: e = pa::launch_decode_d256(l); break;
-  }
-  return e == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+  return pa::launch_decode(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
 
 }  // namespace
@@ -275,15 +312,15 @@ const char* pa_status_string(pa_status_t s) {
     case PA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case PA_ERR_BAD_SHAPE: return "tensor sizes are inconsistent or out of range";
     case PA_ERR_BAD_BLOCK_SIZE: return "block_size must divide TILE and be a multiple of 8 (16 for int8)";
-    case PA_ERR_UNSUPPORTED: return "head_dim must be 64, 128 or 256 and x must be 8";
-    case PA_ERR_WORKSPACE: return "workspace is NULL, misaligned or smaller than required";
+    case PA_ERR_UNSUPPORTED: return "head_dim must be 64, 80, 96, 112, 128 or 256 and x must be 8";
+    case PA_ERR_WORKSPACE: return "counters or workspace NULL, misaligned or smaller than required";
     case PA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
     case PA_ERR_EMPTY_CONTEXT: return "context_lens must be >= 1 (empty sequences unsupported)";
   }
   return "unknown status";
 }
 
-const char* pa_version(void) { return "pa_mi355x 0.1 (gfx950)"; }
+const char* pa_version(void) { return "pa_mi355x 0.2 (gfx950)"; }
 
 pa_status_t pa_validate_decode(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
                                int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks,
@@ -343,7 +380,7 @@ size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_
 
 pa_status_t pa_decode_set_waves_per_group(int32_t waves) {
   if (waves != 0 && waves != 4 && waves != 8) return PA_ERR_BAD_SHAPE;
-  g_waves_override.store(waves, std::memory_order_relaxed);
+  g_waves_override = waves;
   return PA_OK;
 }
 
@@ -356,71 +393,60 @@ size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_
 
 pa_status_t pa_decode_set_schedule(int32_t mode) {
   if (mode < 0 || mode > 2) return PA_ERR_BAD_SHAPE;
-  g_schedule_mode.store(mode, std::memory_order_relaxed);
+  g_schedule_mode = mode;
   return PA_OK;
 }
 
 pa_status_t pa_decode_set_load_policy(int32_t mode) {
   if (mode < 0 || mode > 2) return PA_ERR_BAD_SHAPE;
-  g_load_mode.store(mode, std::memory_order_relaxed);
+  g_load_mode = mode;
   return PA_OK;
 }
 
-pa_status_t pa_paged_decode_attn_warp(void* out, const void* q, const void* k_cache,
-                                      const void* v_cache, const int32_t* block_table,
-                                      const int32_t* context_lens, float scale,
-                                      int32_t block_size, int32_t num_seqs, int32_t num_heads,
-                                      int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks,
-                                      int32_t x, int32_t max_blocks_per_seq,
-                                      int32_t max_context_len, int32_t partition_tokens,
-                                      void* workspace, size_t workspace_bytes,
-                                      pa_stream_t stream) {
-  return decode_common(PA_DECODE_WARP_F16, out, q, k_cache, v_cache, nullptr, nullptr,
-                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
-                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
-                       partition_tokens, workspace, workspace_bytes, stream);
+pa_status_t pa_decode_counters_reset(void* counters, size_t bytes, pa_stream_t stream) {
+  if (bytes == 0) return PA_OK;
+  if (!counters) return PA_ERR_NULL_POINTER;
+  if (bytes % 4 != 0 || reinterpret_cast<uintptr_t>(counters) % 4 != 0) return PA_ERR_BAD_SHAPE;
+  return pa::launch_fill_zero(counters, bytes, reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? PA_OK
+             : PA_ERR_LAUNCH;
 }
 
-pa_status_t pa_paged_decode_attn_splitk(void* out, const void* q, const void* k_cache,
-                                        const void* v_cache, const int32_t* block_table,
-                                        const int32_t* context_lens, float scale,
-                                        int32_t block_size, int32_t num_seqs, int32_t num_heads,
-                                        int32_t head_dim, int32_t num_kv_heads,
-                                        int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
-                                        int32_t max_context_len, int32_t partition_tokens,
-                                        void* workspace, size_t workspace_bytes,
-                                        pa_stream_t stream) {
-  return decode_common(PA_DECODE_SPLITK_F16, out, q, k_cache, v_cache, nullptr, nullptr,
-                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
-                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
-                       partition_tokens, workspace, workspace_bytes, stream);
-}
+// The four decode entry points differ only in the kind they pass on.
+#define PA_DECODE_ENTRY_F16(NAME, KIND)                                                          \
+  pa_status_t NAME(void* out, const void* q, const void* k_cache, const void* v_cache,          \
+                   const int32_t* block_table, const int32_t* context_lens, float scale,        \
+                   int32_t block_size, int32_t num_seqs, int32_t num_heads, int32_t head_dim,   \
+                   int32_t num_kv_heads, int32_t num_blocks, int32_t x,                         \
+                   int32_t max_blocks_per_seq, int32_t max_context_len,                         \
+                   int32_t partition_tokens, void* counters, size_t counter_bytes,              \
+                   void* workspace, size_t workspace_bytes, pa_stream_t stream) {               \
+    return decode_common(KIND, out, q, k_cache, v_cache, nullptr, nullptr, block_table,         \
+                         context_lens, scale, block_size, num_seqs, num_heads, head_dim,        \
+                         num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,      \
+                         partition_tokens, counters, counter_bytes, workspace, workspace_bytes, \
+                         stream);                                                               \
+  }
+#define PA_DECODE_ENTRY_I8(NAME, KIND)                                                           \
+  pa_status_t NAME(void* out, const void* q, const void* k_cache, const void* v_cache,          \
+                   const float* k_scales, const float* v_scales, const int32_t* block_table,    \
+                   const int32_t* context_lens, float scale, int32_t block_size,                \
+                   int32_t num_seqs, int32_t num_heads, int32_t head_dim,                       \
+                   int32_t num_kv_heads, int32_t num_blocks, int32_t x,                         \
+                   int32_t max_blocks_per_seq, int32_t max_context_len,                         \
+                   int32_t partition_tokens, void* counters, size_t counter_bytes,              \
+                   void* workspace, size_t workspace_bytes, pa_stream_t stream) {               \
+    return decode_common(KIND, out, q, k_cache, v_cache, k_scales, v_scales, block_table,       \
+                         context_lens, scale, block_size, num_seqs, num_heads, head_dim,        \
+                         num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,      \
+                         partition_tokens, counters, counter_bytes, workspace, workspace_bytes, \
+                         stream);                                                               \
+  }
 
-pa_status_t pa_paged_decode_attn_warp_int8(
-    void* out, const void* q, const void* k_cache, const void* v_cache, const float* k_scales,
-    const float* v_scales, const int32_t* block_table, const int32_t* context_lens, float scale,
-    int32_t block_size, int32_t num_seqs, int32_t num_heads, int32_t head_dim,
-    int32_t num_kv_heads, int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
-    int32_t max_context_len, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
-    pa_stream_t stream) {
-  return decode_common(PA_DECODE_WARP_I8, out, q, k_cache, v_cache, k_scales, v_scales,
-                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
-                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
-                       partition_tokens, workspace, workspace_bytes, stream);
-}
-
-pa_status_t pa_paged_decode_attn_splitk_int8(
-    void* out, const void* q, const void* k_cache, const void* v_cache, const float* k_scales,
-    const float* v_scales, const int32_t* block_table, const int32_t* context_lens, float scale,
-    int32_t block_size, int32_t num_seqs, int32_t num_heads, int32_t head_dim,
-    int32_t num_kv_heads, int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq,
-    int32_t max_context_len, int32_t partition_tokens, void* workspace, size_t workspace_bytes,
-    pa_stream_t stream) {
-  return decode_common(PA_DECODE_SPLITK_I8, out, q, k_cache, v_cache, k_scales, v_scales,
-                       block_table, context_lens, scale, block_size, num_seqs, num_heads,
-                       head_dim, num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,
-                       partition_tokens, workspace, workspace_bytes, stream);
-}
+PA_DECODE_ENTRY_F16(pa_paged_decode_attn_warp, PA_DECODE_WARP_F16)
+PA_DECODE_ENTRY_F16(pa_paged_decode_attn_splitk, PA_DECODE_SPLITK_F16)
+PA_DECODE_ENTRY_I8(pa_paged_decode_attn_warp_int8, PA_DECODE_WARP_I8)
+PA_DECODE_ENTRY_I8(pa_paged_decode_attn_splitk_int8, PA_DECODE_SPLITK_I8)
 
 }  // extern "C"
 

@@ -1,0 +1,19 @@
+// Decode kernels instantiated for one head_dim: this file is compiled once
+// per supported head_dim with -DPA_HEAD_DIM=<D> (every kind, FP16 and INT8).
+#include "pa_decode_kernels.hpp"
+
+#ifndef PA_HEAD_DIM
+#error "compile once per head_dim with -DPA_HEAD_DIM=<D>"
+#endif
+
+#define PA_CAT_(a, b) a##b
+#define PA_CAT(a, b) PA_CAT_(a, b)
+
+namespace pa {
+hipError_t PA_CAT(launch_decode_d, PA_HEAD_DIM)(const DecodeLaunch& l) {
+  return launch_decode_d<PA_HEAD_DIM>(l);
+}
+int PA_CAT(sched_groups_d, PA_HEAD_DIM)(int waves, bool int8_kv) {
+  return sched_groups_d<PA_HEAD_DIM>(waves, int8_kv);
+}
+}  // namespace pa

@@ -256,8 +256,15 @@ __device__ __forceinline__ void decode_split(
     half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
     uint32_t* __restrict__ cnt, const DecodeShape& sh, SplitWork wk,
     DecodeSmem<D, NW>& sm, Resolve&& resolve, AfterIssue&& after_issue) {
-  constexpr int KC = D / 32;                 // 32-dim k-chunks of one QK product
+  static_assert(D % 16 == 0 && D >= 64 && D <= 256, "head_dim: a multiple of 16 in [64, 256]");
+  constexpr int KC = (D + 31) / 32;          // 32-dim k-chunks of one QK product
   constexpr int NT = D / 16;                 // 16-dim output tiles of PV
+  constexpr int DG = D / 8;                  // 8-dim groups of a K row
+  // With head_dim % 32 == 16 the last k-chunk holds 16 dims: its dim groups
+  // 4(KC-1) + g for g >= 2 lie past the row.  Those lanes load the row's last
+  // group instead (in bounds) and feed zeros to the MFMA; their query
+  // operand is zero as well.
+  constexpr bool KPAD = (D % 32) != 0;
   constexpr int PAIRS = D <= 128 ? 2 : 1;    // 32-token pairs per wave iteration
   constexpr int IT = 32 * PAIRS;             // tokens per wave iteration
   constexpr int ESZ = I8 ? 1 : 2;            // bytes per cache element
@@ -314,7 +321,9 @@ __device__ __forceinline__ void decode_split(
     const half_t* qrow = q + ((size_t)seq * sh.num_heads + head0 + (hv ? r : 0)) * D + 8 * g;
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
-      const uint4 v = hv ? *reinterpret_cast<const uint4*>(qrow + 32 * kk) : make_uint4(0, 0, 0, 0);
+      const bool dv = !KPAD || kk < KC - 1 || 4 * kk + g < DG;
+      const uint4 v = (hv && dv) ? *reinterpret_cast<const uint4*>(qrow + 32 * kk)
+                                 : make_uint4(0, 0, 0, 0);
       qreg[kk] = __builtin_bit_cast(h8_t, v);
     }
   }
@@ -375,6 +384,10 @@ __device__ __forceinline__ void decode_split(
   };
   W8Buf wa;
 
+  // Dim-group offset (relative to the lane's group g) of k-chunk kk's K row
+  // load: 4 kk, or for the padding lanes of a 16-dim last chunk the row's
+  // last group.
+  auto kgroup = [&](int kk) { return (!KPAD || 4 * kk + g < DG) ? 4 * kk : DG - 1 - g; };
   auto load_blocks = [&](int it_, Blocks& b) {
     const int tok0 = t_begin + it_ * IT;
     if constexpr (W8) {
@@ -413,7 +426,7 @@ __device__ __forceinline__ void decode_split(
       for (int p = 0; p < PAIRS; ++p)
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk)
-          kw[p][kk] = load_tile<uint4, KNT>(kp + (size_t)(4 * kk) * bs * 8 + 64 * p);
+          kw[p][kk] = load_tile<uint4, KNT>(kp + (size_t)kgroup(kk) * bs * 8 + 64 * p);
       return;
     }
 #pragma unroll
@@ -425,7 +438,7 @@ __device__ __forceinline__ void decode_split(
       const uint8_t* kp = kc + ((((size_t)kb * hkv + kvh) * (D / 8) + g) * bs + koff) * 8 * ESZ;
 #pragma unroll
       for (int kk = 0; kk < KC; ++kk) {
-        const uint8_t* p0 = kp + (size_t)(4 * kk) * bs * 8 * ESZ;
+        const uint8_t* p0 = kp + (size_t)kgroup(kk) * bs * 8 * ESZ;
         kx[p][kk] = load_tile<LVec, KNT>(p0);
         ky[p][kk] = load_tile<LVec, KNT>(p0 + 4 * 8 * ESZ);
       }
@@ -632,6 +645,10 @@ __device__ __forceinline__ void decode_split(
           } else {
             ax = __builtin_bit_cast(h8_t, kx[p][kk]);
             ay = __builtin_bit_cast(h8_t, ky[p][kk]);
+          }
+          if (KPAD && kk == KC - 1 && 4 * kk + g >= DG) {
+            ax = (h8_t){};   // padding lanes of the last k-chunk (their q is zero too)
+            ay = (h8_t){};
           }
           sx = mfma16(ax, qreg[kk], sx);
           sy = mfma16(ay, qreg[kk], sy);

@@ -79,16 +79,22 @@ struct DecodeLaunch {
   hipStream_t stream;
 };
 
-// Resident work-groups of the scheduled decode kernel (0 if it cannot run).
-// Defined in pa_decode_d{64,128,256}.hip.
-int sched_groups_d64(int waves, bool int8_kv);
-int sched_groups_d128(int waves, bool int8_kv);
-int sched_groups_d256(int waves, bool int8_kv);
+// Head dims the library is built for.  The decode kernels are instantiated
+// once per head_dim from pa_decode_inst.hip (compiled with -DPA_HEAD_DIM=D);
+// the write kernels take the same set.
+#define PA_FOR_EACH_HEAD_DIM(X) X(64) X(80) X(96) X(112) X(128) X(256)
 
-// Defined in pa_decode_d{64,128,256}.hip.
-hipError_t launch_decode_d64(const DecodeLaunch& l);
-hipError_t launch_decode_d128(const DecodeLaunch& l);
-hipError_t launch_decode_d256(const DecodeLaunch& l);
+// Per head_dim D: the launcher of every decode kind, and the resident
+// work-groups of the scheduled decode kernel (0 if it cannot run).
+#define PA_DECLARE_DECODE_D(D)                               \
+  hipError_t launch_decode_d##D(const DecodeLaunch& l);      \
+  int sched_groups_d##D(int waves, bool int8_kv);
+PA_FOR_EACH_HEAD_DIM(PA_DECLARE_DECODE_D)
+#undef PA_DECLARE_DECODE_D
+
+// Zeroes `bytes` (a multiple of 4) at `p` with a fill kernel on `stream`
+// (pa_fill.hip).  A HIP graph may capture it: no memset node is recorded.
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
 struct QuantLaunch {
   const void* key;

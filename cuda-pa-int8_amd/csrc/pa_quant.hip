@@ -151,9 +151,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(void* base, uint32_t
 }
 
 // The 16-B input groups of one job for one lane, and the lane's token slot.
+// Lane quarter qq owns the dim groups qq + 4j; with head_dim % 32 == 16 the
+// last j holds a group only for qq < 2 (the others load the row's last group,
+// in bounds, and ignore it).
 template <int D>
 struct QuantJob {
-  static constexpr int JQ = D / 32;   // 16-B groups per lane
+  static constexpr int DG = D / 8;          // 8-dim groups of a row
+  static constexpr int JQ = (DG + 3) / 4;   // 16-B groups per lane
   uint4 x[JQ];
   int64_t slot;
 };
@@ -168,7 +172,9 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
                    int num_blocks, int bs, int bs_log2, int njobs, const float* __restrict__ k_scale_in,
                    const float* __restrict__ v_scale_in) {
+  static_assert(D % 16 == 0, "head_dim must be a multiple of 16");
   constexpr int JQ = QuantJob<D>::JQ;
+  constexpr int DG = QuantJob<D>::DG;
   __shared__ __attribute__((aligned(16))) uint8_t tile[kQuantWaves][D * 16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -192,7 +198,10 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     const half_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
                              : key + (int64_t)tc * kts + (int64_t)h * khs;
 #pragma unroll
-    for (int j = 0; j < JQ; ++j) J.x[j] = load_stream<uint4>(src + (qq + 4 * j) * 8);   // read once
+    for (int j = 0; j < JQ; ++j) {
+      const int o = qq + 4 * j < DG ? qq + 4 * j : DG - 1;
+      J.x[j] = load_stream<uint4>(src + o * 8);   // read once
+    }
   };
 
   // Two jobs stay in flight ahead of the one being quantized.  A prefetch
@@ -230,6 +239,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       u16x2_t am2 = {0, 0};
 #pragma unroll
       for (int j = 0; j < JQ; ++j) {
+        if (qq + 4 * j >= DG) continue;   // a padding group (duplicate of the last one)
         const uint32_t wv[4] = {cur.x[j].x, cur.x[j].y, cur.x[j].z, cur.x[j].w};
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -272,6 +282,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     // One 16-B group at a time: quantize, fix rare elements exactly, store.
 #pragma unroll
     for (int j = 0; j < JQ; ++j) {
+      if (qq + 4 * j >= DG) continue;   // padding group: nothing to write
       bool slow = !s_normal;
       uint2 qj = STATIC ? quant_group_fast_sat(cur.x[j], r, slow)
                         : quant_group_fast(cur.x[j], r, slow);
@@ -373,9 +384,10 @@ static hipError_t launch_quant_d(const QuantLaunch& l) {
 template <bool STATIC>
 static hipError_t launch_quant(const QuantLaunch& l) {
   switch (l.head_dim) {
-    case 64: return launch_quant_d<64, STATIC>(l);
-    case 128: return launch_quant_d<128, STATIC>(l);
-    case 256: return launch_quant_d<256, STATIC>(l);
+#define PA_CASE(D) \
+  case D: return launch_quant_d<D, STATIC>(l);
+    PA_FOR_EACH_HEAD_DIM(PA_CASE)
+#undef PA_CASE
     default: return hipErrorInvalidValue;
   }
 }

@@ -10,6 +10,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "pa_mi355x.h"
 
@@ -17,38 +18,52 @@ namespace {
 
 constexpr int64_t kRefTile = 128;
 
-// One zero-initialised workspace per (device, stream), grown on demand; calls
-// on one stream are ordered by the stream itself.  A call needs its counter
-// region -- the first pa_decode_counter_bytes(...) bytes for its shape -- to be
-// zero, and leaves exactly that region zero; the bytes after it hold split
-// partials.  `zero_prefix` is the length known to be zero, so when a later
-// shape needs a longer counter region, the bytes between are cleared first
-// (with a fill kernel, which a HIP graph may also capture).
-struct Workspace {
+// Device memory of a decode call (include/pa_mi355x.h):
+//
+// * Counters: one buffer per (device, stream), zeroed when it is made; every
+//   call leaves its counters zero again, so calls of any shape share it.  It
+//   only grows, and a superseded buffer is kept until the process ends: a HIP
+//   graph captured earlier may still hold its address.  A buffer first made
+//   while the stream is being captured is zeroed by the captured fill only
+//   when the graph replays, so the next call outside a capture zeroes it once
+//   more before using it.
+// * Workspace (split partials, schedule record): plain scratch, allocated per
+//   call from the stream-ordered caching allocator as the reference does for
+//   its partials (kernels/paged_attention_v4_splitk.cu:216-219).  Under graph
+//   capture it comes from the graph's private pool and stays valid for every
+//   replay; graphs never share it.
+struct Counters {
   at::Tensor buf;
-  size_t zero_prefix = 0;
+  bool zeroed_eagerly = false;
+  std::vector<at::Tensor> retired;
 };
-std::mutex g_ws_mu;
-std::map<std::pair<int, void*>, Workspace> g_ws;
+std::mutex g_counters_mu;
+std::map<std::pair<int, void*>, Counters> g_counters;
+constexpr size_t kMinCounterBytes = 256 << 10;   // 65k units: grows only for huge batches
 
-at::Tensor workspace_for(const at::Tensor& like, hipStream_t stream, size_t bytes,
-                         size_t counter_bytes) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  const auto key = std::make_pair((int)like.get_device(), (void*)stream);
-  auto it = g_ws.find(key);
-  if (it == g_ws.end() || (size_t)it->second.buf.numel() < bytes) {
-    size_t want = std::max<size_t>(bytes, 1 << 20);
-    if (it != g_ws.end()) want = std::max<size_t>(want, 2 * (size_t)it->second.buf.numel());
-    Workspace w;
-    w.buf = at::zeros({(int64_t)want}, like.options().dtype(at::kByte));
-    w.zero_prefix = want;
-    it = g_ws.insert_or_assign(key, w).first;
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  TORCH_CHECK(hipStreamIsCapturing(stream, &st) == hipSuccess, "hipStreamIsCapturing failed");
+  return st != hipStreamCaptureStatusNone;
+}
+
+at::Tensor counters_for(const at::Tensor& like, hipStream_t stream, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_counters_mu);
+  Counters& c = g_counters[std::make_pair((int)like.get_device(), (void*)stream)];
+  const bool capturing = stream_capturing(stream);
+  if (!c.buf.defined() || (size_t)c.buf.numel() < bytes) {
+    size_t want = std::max(bytes, kMinCounterBytes);
+    if (c.buf.defined()) {
+      want = std::max(want, 2 * (size_t)c.buf.numel());
+      c.retired.push_back(c.buf);
+    }
+    c.buf = at::zeros({(int64_t)want}, like.options().dtype(at::kByte));
+    c.zeroed_eagerly = !capturing;
+  } else if (!c.zeroed_eagerly && !capturing) {
+    c.buf.zero_();
+    c.zeroed_eagerly = true;
   }
-  Workspace& w = it->second;
-  if (counter_bytes > w.zero_prefix)
-    w.buf.narrow(0, (int64_t)w.zero_prefix, (int64_t)(counter_bytes - w.zero_prefix)).zero_();
-  w.zero_prefix = counter_bytes;   // the partials after it are written by this call
-  return w.buf;
+  return c.buf;
 }
 
 void check_status(pa_status_t st) { TORCH_CHECK(st == PA_OK, pa_status_string(st)); }
@@ -142,38 +157,37 @@ void run_decode(pa_decode_kind_t kind, at::Tensor& out, const at::Tensor& q,
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
   const size_t need = pa_decode_workspace_bytes(kind, S, H, D, Hkv, (int32_t)block_size, MB,
                                                 max_ctx, (int32_t)partition_tokens);
-  at::Tensor ws = workspace_for(q, stream, need, pa_decode_counter_bytes(S, H, Hkv));
+  const size_t cneed = pa_decode_counter_bytes(S, H, Hkv);
+  at::Tensor cnt = counters_for(q, stream, cneed);
+  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(need, 256)}, q.options().dtype(at::kByte));
   const float sc = (float)scale;
-  pa_status_t st;
   auto ps = reinterpret_cast<pa_stream_t>(stream);
+  void* o = out.data_ptr();
+  const void *qp = q.data_ptr(), *kp = k_cache.data_ptr(), *vp = v_cache.data_ptr();
+  const int32_t* bt = block_table.data_ptr<int32_t>();
+  const int32_t* cl = context_lens.data_ptr<int32_t>();
+  const int32_t bs = (int32_t)block_size, xx = (int32_t)x, pt = (int32_t)partition_tokens;
+  void *cp = cnt.data_ptr(), *wp = ws.data_ptr();
+  const size_t cb = cnt.numel(), wb = ws.numel();
+  pa_status_t st;
   switch (kind) {
     case PA_DECODE_WARP_F16:
-      st = pa_paged_decode_attn_warp(out.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
-                                     v_cache.data_ptr(), block_table.data_ptr<int32_t>(),
-                                     context_lens.data_ptr<int32_t>(), sc, (int32_t)block_size, S,
-                                     H, D, Hkv, NB, (int32_t)x, MB, max_ctx,
-                                     (int32_t)partition_tokens, ws.data_ptr(), ws.numel(), ps);
+      st = pa_paged_decode_attn_warp(o, qp, kp, vp, bt, cl, sc, bs, S, H, D, Hkv, NB, xx, MB,
+                                     max_ctx, pt, cp, cb, wp, wb, ps);
       break;
     case PA_DECODE_SPLITK_F16:
-      st = pa_paged_decode_attn_splitk(out.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
-                                       v_cache.data_ptr(), block_table.data_ptr<int32_t>(),
-                                       context_lens.data_ptr<int32_t>(), sc, (int32_t)block_size,
-                                       S, H, D, Hkv, NB, (int32_t)x, MB, max_ctx,
-                                       (int32_t)partition_tokens, ws.data_ptr(), ws.numel(), ps);
+      st = pa_paged_decode_attn_splitk(o, qp, kp, vp, bt, cl, sc, bs, S, H, D, Hkv, NB, xx, MB,
+                                       max_ctx, pt, cp, cb, wp, wb, ps);
       break;
     case PA_DECODE_WARP_I8:
-      st = pa_paged_decode_attn_warp_int8(
-          out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-          k_scales->data_ptr<float>(), v_scales->data_ptr<float>(), block_table.data_ptr<int32_t>(),
-          context_lens.data_ptr<int32_t>(), sc, (int32_t)block_size, S, H, D, Hkv, NB, (int32_t)x,
-          MB, max_ctx, (int32_t)partition_tokens, ws.data_ptr(), ws.numel(), ps);
+      st = pa_paged_decode_attn_warp_int8(o, qp, kp, vp, k_scales->data_ptr<float>(),
+                                          v_scales->data_ptr<float>(), bt, cl, sc, bs, S, H, D,
+                                          Hkv, NB, xx, MB, max_ctx, pt, cp, cb, wp, wb, ps);
       break;
     default:
-      st = pa_paged_decode_attn_splitk_int8(
-          out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-          k_scales->data_ptr<float>(), v_scales->data_ptr<float>(), block_table.data_ptr<int32_t>(),
-          context_lens.data_ptr<int32_t>(), sc, (int32_t)block_size, S, H, D, Hkv, NB, (int32_t)x,
-          MB, max_ctx, (int32_t)partition_tokens, ws.data_ptr(), ws.numel(), ps);
+      st = pa_paged_decode_attn_splitk_int8(o, qp, kp, vp, k_scales->data_ptr<float>(),
+                                            v_scales->data_ptr<float>(), bt, cl, sc, bs, S, H, D,
+                                            Hkv, NB, xx, MB, max_ctx, pt, cp, cb, wp, wb, ps);
       break;
   }
   check_status(st);
@@ -385,7 +399,14 @@ PYBIND11_MODULE(paged_attn_opt, m) {
   m.def("reshape_and_cache_int8_static", &reshape_and_cache_int8_static,
         "INT8 quantize with one given scale per K / V tensor + paged cache write (new op)");
   m.def("reshape_and_cache", &reshape_and_cache, "fp16 paged cache write (new op)");
-  m.def("set_waves_per_group", [](int64_t w) { check_status(pa_decode_set_waves_per_group((int32_t)w)); },
-        "tuning hook: force 4 or 8 waves per decode work-group (0 = automatic)");
   m.def("version", []() { return std::string(pa_version()); });
+}
+
+// The reference builds its naive stage as a module of its own,
+// paged_attn_naive (kernels/paged_attention_naive.cu:169-172).  The same
+// shared object also initialises under that name, with that one op.
+PYBIND11_MODULE(paged_attn_naive, m) {
+  m.def("paged_decode_attention", &paged_decode_attention,
+        "paged decode (FP16 KV), the naive stage's module and entry name; single-launch kernel, "
+        "gfx950");
 }

@@ -4,6 +4,9 @@
   ``include/pa_mi355x.h`` (hipcc, ``--offload-arch=gfx950``).
 * ``lib/paged_attn_opt.so`` -- the thin torch extension (g++ against
   torch's headers), linked to the library above with an ``$ORIGIN`` rpath.
+  The same object also initialises as ``paged_attn_naive``.
+* ``lib/libpa_bench_probe.so`` -- streaming-rate probes the benchmark uses
+  (``csrc/bench/``); not part of the decode path.
 
 Object files go to ``_build/`` next to this package.  Every call rebuilds
 from source; nothing is fetched.
@@ -29,16 +32,18 @@ ARCH = "gfx950"
 
 LIB_NAME = "libpa_mi355x.so"
 EXT_NAME = "paged_attn_opt.so"
+PROBE_LIB_NAME = "libpa_bench_probe.so"
 
+# head_dims of the decode kernels: pa_decode_inst.hip is compiled once per
+# entry (keep in step with PA_FOR_EACH_HEAD_DIM in csrc/pa_internal.hpp).
+HEAD_DIMS = (64, 80, 96, 112, 128, 256)
 HIP_SOURCES = [
-    "pa_decode_d64.hip",
-    "pa_decode_d128.hip",
-    "pa_decode_d256.hip",
     "pa_quant.hip",
     "pa_cache_write.hip",
-    "pa_probe.hip",
+    "pa_fill.hip",
 ]
 HOST_SOURCES = ["pa_capi.cpp"]
+PROBE_SOURCES = ["bench/pa_probe.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -73,24 +78,45 @@ def _hipcc():
     return os.path.join(ROCM, "bin", "hipcc")
 
 
+def _compile_cmd(src, obj, defines=()):
+    extra = ["-x", "hip"] if src.endswith(".hip") else []
+    return [_hipcc(), *HIPCC_FLAGS, *defines, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+
+
+def _link(objs, name, verbose, libs=()):
+    out = os.path.join(LIB_DIR, name)
+    tmp = out + ".tmp"
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *libs,
+          f"-Wl,-rpath,{ROCM}/lib", f"-Wl,-soname,{name}"], verbose)
+    os.replace(tmp, out)
+    return out
+
+
 def build_library(verbose=False, jobs=None):
-    os.makedirs(OBJ_DIR, exist_ok=True)
+    """Compile every HIP / host source of the library (and the probe library)
+    in parallel, then link both."""
+    os.makedirs(os.path.join(OBJ_DIR, "bench"), exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     jobs = jobs or max(1, min(8, int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
-    cmds, objs = [], []
+    cmds, objs, probe_objs = [], [], []
+    for d in HEAD_DIMS:
+        obj = os.path.join(OBJ_DIR, f"pa_decode_d{d}.o")
+        objs.append(obj)
+        cmds.append(_compile_cmd("pa_decode_inst.hip", obj, [f"-DPA_HEAD_DIM={d}"]))
     for src in HIP_SOURCES + HOST_SOURCES:
         obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        extra = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([_hipcc(), *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append(_compile_cmd(src, obj))
+    for src in PROBE_SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        probe_objs.append(obj)
+        cmds.append(_compile_cmd(src, obj))
+    # the slowest units (the decode instantiations) first
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for f in [ex.submit(_run, c, verbose) for c in cmds]:
             f.result()
-    out = os.path.join(LIB_DIR, LIB_NAME)
-    tmp = out + ".tmp"
-    _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-          f"-Wl,-rpath,{ROCM}/lib", f"-Wl,-soname,{LIB_NAME}"], verbose)
-    os.replace(tmp, out)
+    out = _link(objs, LIB_NAME, verbose)
+    _link(probe_objs, PROBE_LIB_NAME, verbose)
     return out
 
 

@@ -16,7 +16,8 @@
  *   block_table   [num_seqs, max_blocks_per_seq]                       int32
  *   context_lens  [num_seqs]                                           int32
  * All arrays are dense and row-major.  kv_head of query head h is
- * h / (num_heads / num_kv_heads).
+ * h / (num_heads / num_kv_heads).  head_dim is one of 64, 80, 96, 112, 128
+ * and 256.
  *
  * Behaviour on data the host cannot see (the caller owns these guarantees;
  * the kernels stay memory-safe when they are broken):
@@ -27,16 +28,20 @@
  *     upper bound of every length, or <= 0);
  *   - a block id outside [0, num_blocks) contributes no tokens.
  *
- * Workspace: the decode entry points need device scratch of
- * pa_decode_workspace_bytes(...) bytes, 256-byte aligned.  Its first
- * pa_decode_counter_bytes(...) bytes for the call's shape are arrival and
- * claim counters that must be zero when the call starts; the call leaves
- * exactly those bytes zero and uses the rest as scratch for split partials.
- * A workspace zeroed at allocation can therefore be reused for calls of one
- * shape without clearing; before a call whose counter region is longer than
- * the previous call's, clear the bytes in between (they held partials).  Two
- * calls that may run at the same time (different streams) need different
- * workspaces.
+ * Device memory of a decode call, both supplied by the caller:
+ *   counters   pa_decode_counter_bytes(...) bytes (or more), 256-byte
+ *              aligned: arrival and claim counters.  They must be zero when a
+ *              call starts, and every call leaves them zero when its kernels
+ *              finish.  Zero them once (pa_decode_counters_reset, or any fill)
+ *              and keep them: calls of any shape may share one counter buffer
+ *              as long as they run one after another (one stream, or replays
+ *              of HIP graphs captured on it that do not overlap).
+ *   workspace  pa_decode_workspace_bytes(...) bytes, 256-byte aligned:
+ *              scratch for split partials and the schedule record.  No
+ *              initial contents are required and nothing is kept between
+ *              calls, so it may come from a stream-ordered allocator per call.
+ * Two calls that may run at the same time need separate counters and
+ * separate workspaces.
  */
 #ifndef PA_MI355X_H
 #define PA_MI355X_H
@@ -56,7 +61,7 @@ typedef enum pa_status {
   PA_ERR_BAD_SHAPE = 2,        /* sizes inconsistent or out of range */
   PA_ERR_BAD_BLOCK_SIZE = 3,   /* block_size rejected (same rule as the reference) */
   PA_ERR_UNSUPPORTED = 4,      /* head_dim / x not built into this library */
-  PA_ERR_WORKSPACE = 5,        /* workspace NULL or smaller than required */
+  PA_ERR_WORKSPACE = 5,        /* counters / workspace NULL, misaligned or too small */
   PA_ERR_LAUNCH = 6,           /* the HIP runtime refused the launch */
   PA_ERR_EMPTY_CONTEXT = 7     /* a context length < 1 (host-side check) */
 } pa_status_t;
@@ -100,41 +105,20 @@ pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_
                            int32_t partition_tokens, int32_t* out_partition_tokens,
                            int32_t* out_num_splits);
 
+/* Scratch bytes of one decode call (the `workspace` argument); 0 for an
+ * invalid shape. */
 size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
                                  int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
                                  int32_t max_blocks_per_seq, int32_t max_context_len,
                                  int32_t partition_tokens);
+/* Counter bytes of one decode call (the `counters` argument), the same for
+ * every kind; 0 for an invalid shape. */
 size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads);
 
-/* Tuning hook (no reference counterpart): force 4 or 8 waves per decode
- * work-group for every later plan in this process; 0 restores the automatic
- * choice (8 for head_dim <= 128, else 4).  Used by partition/occupancy
- * sweeps; affects pa_decode_plan, pa_decode_workspace_bytes and the launches
- * alike, so set it before sizing a workspace. */
-pa_status_t pa_decode_set_waves_per_group(int32_t waves);
-
-/* Tuning hook (no reference counterpart): how later decode calls in this
- * process distribute work.  0 = automatic: the in-kernel schedule for the
- * split-K kinds with up to 1024 sequences, the grid otherwise; 1 = grid: one
- * work-group per (unit, split) slot of the host plan; 2 = in-kernel schedule:
- * persistent work-groups, one per resident slot, claim (split, kv head, head
- * chunk) items of a compact work list that every work-group derives from
- * context_lens, so no work-group is launched for a split a sequence does not
- * have and the partition follows the actual lengths.  Set it before sizing a
- * workspace. */
-pa_status_t pa_decode_set_schedule(int32_t mode);
-
-/* Tuning hook (no reference counterpart): how later decode calls in this
- * process load V cache rows.  (K rows use plain loads, since each K line is
- * read by two consecutive load instructions, except in FP16 grid launches
- * whose splits hold at least 4096 tokens, which load K non-temporally too
- * whenever V is.)  0 = automatic: non-temporal loads when each
- * kv head's tiles are read by one work-group (query heads per kv head <= 16)
- * and the call reads more than 32 MB of K/V; plain loads when several head
- * chunks share the tiles through the L2, or when a small cache may still sit
- * in the Infinity Cache from an earlier call; 1 = plain; 2 = non-temporal.
- * Results do not depend on it. */
-pa_status_t pa_decode_set_load_policy(int32_t mode);
+/* Zeroes `bytes` (a multiple of 4) of a counter buffer on `stream` with a
+ * fill kernel (no memset node, so a HIP graph may capture it).  For a new
+ * buffer, or one whose last call did not run to completion. */
+pa_status_t pa_decode_counters_reset(void* counters, size_t bytes, pa_stream_t stream);
 
 /* FP16 KV, single launch.  Replaces paged_decode_attn_warp
  * (kernels/paged_attention_v3_warp.cu:137-176; bound at kernels/bindings.cpp:50-51).
@@ -146,7 +130,8 @@ pa_status_t pa_paged_decode_attn_warp(
     const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
     int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
     int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
-    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+    int32_t partition_tokens, void* counters, size_t counter_bytes, void* workspace,
+    size_t workspace_bytes, pa_stream_t stream);
 
 /* FP16 KV, split-K: a partition kernel writes per-split (acc, max, sum)
  * partials and a separate reduce kernel merges them.  Replaces
@@ -157,7 +142,8 @@ pa_status_t pa_paged_decode_attn_splitk(
     const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
     int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
     int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
-    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+    int32_t partition_tokens, void* counters, size_t counter_bytes, void* workspace,
+    size_t workspace_bytes, pa_stream_t stream);
 
 /* INT8 KV with per-(token, kv_head) fp32 scales, single launch.  Replaces
  * paged_decode_attn_warp_int8 (kernels/paged_attention_v5_warp_int8.cu:150-197;
@@ -168,7 +154,8 @@ pa_status_t pa_paged_decode_attn_warp_int8(
     const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
     int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
     int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
-    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+    int32_t partition_tokens, void* counters, size_t counter_bytes, void* workspace,
+    size_t workspace_bytes, pa_stream_t stream);
 
 /* INT8 KV, split-K partition + reduce.  Replaces paged_decode_attn_splitk_int8
  * (kernels/paged_attention_v6_splitk_int8.cu:194-259; bindings.cpp:56-57). */
@@ -178,7 +165,8 @@ pa_status_t pa_paged_decode_attn_splitk_int8(
     const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
     int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
     int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
-    int32_t partition_tokens, void* workspace, size_t workspace_bytes, pa_stream_t stream);
+    int32_t partition_tokens, void* counters, size_t counter_bytes, void* workspace,
+    size_t workspace_bytes, pa_stream_t stream);
 
 /* Per-token INT8 quantize + paged-cache write.  NEW API: the reference has
  * no kernel for it; its semantics are those of quantize_per_token
@@ -227,24 +215,6 @@ pa_status_t pa_reshape_and_cache_f16(
     int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
     void* k_cache, void* v_cache, int32_t num_blocks, int32_t block_size, int32_t x,
     pa_stream_t stream);
-
-/* Measurement helpers (no reference counterpart): streaming probes that give
- * bench.py the practical HBM rates next to the decode and write numbers.
- * pa_probe_read_contiguous sweeps `bytes` from `src` with 16-byte loads;
- * pa_probe_read_chunks reads `num_chunks` chunks of `chunk_bytes` (1024,
- * 2048 or a multiple of 4096) at src + order[i] * chunk_bytes, skipping order
- * values past `bytes`.  Both keep a checksum that is written to `sink` only on a
- * practically impossible value, so the loads cannot be optimised away. */
-pa_status_t pa_probe_read_contiguous(const void* src, size_t bytes, uint32_t* sink, int32_t grid,
-                                     pa_stream_t stream);
-pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* order,
-                                 int32_t num_chunks, int32_t chunk_bytes, uint32_t* sink,
-                                 int32_t grid, pa_stream_t stream);
-/* pa_probe_read_write reads `read_bytes` (a multiple of 16) from `src` and
- * writes read_bytes / 2 to `dst` (below 4 GiB), both contiguous: the
- * practical rate of a stream with the INT8 write kernel's read : write ratio. */
-pa_status_t pa_probe_read_write(const void* src, size_t read_bytes, void* dst, int32_t grid,
-                                pa_stream_t stream);
 
 #ifdef __cplusplus
 }

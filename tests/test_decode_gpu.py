@@ -18,8 +18,8 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import (ATOL, CONTEXT_LENS, GQA, LONG_CONTEXT_LENS, NUM_SEQS, RTOL, assert_close,
-                    fp16_case, int8_case, make_lens, oracle_fp16, oracle_int8)
+from _cases import (ATOL, CONTEXT_LENS, GQA, HEAD_DIMS, LONG_CONTEXT_LENS, NUM_SEQS, RTOL,
+                    assert_close, fp16_case, int8_case, make_lens, oracle_fp16, oracle_int8)
 
 pytestmark = pytest.mark.gpu
 
@@ -133,11 +133,31 @@ def test_fp16_forced_partition(variant, partition, clen):
 
 
 @pytest.mark.parametrize("variant", F16_VARIANTS)
-@pytest.mark.parametrize("head_dim", [64, 256])
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
 @pytest.mark.parametrize("clen", [17, 700])
-def test_fp16_head_dims(variant, head_dim, clen):
-    c = fp16_case(2, make_lens(clen, 2), 8, 2, head_dim=head_dim, seed=5)
+@pytest.mark.parametrize("num_heads,num_kv_heads", [(8, 2), (32, 1)])
+def test_fp16_head_dims(variant, head_dim, clen, num_heads, num_kv_heads):
+    c = fp16_case(2, make_lens(clen, 2), num_heads, num_kv_heads, head_dim=head_dim, seed=5)
     assert_close(run_fp16(c, variant), oracle_fp16(c), what=f"{variant} D={head_dim}")
+
+
+@pytest.mark.parametrize("variant", F16_VARIANTS)
+@pytest.mark.parametrize("head_dim", [80, 96, 112])
+def test_fp16_head_dims_forced_splits(variant, head_dim):
+    """Head dims that are not a multiple of 32 (masked last QK chunk) across
+    many splits, both work distributions."""
+    import pa_int8
+
+    lib = pa_int8.capi()
+    c = fp16_case(3, make_lens(2100, 3), 12, 2, head_dim=head_dim, seed=6)
+    want = oracle_fp16(c)
+    try:
+        for mode in (1, 2):
+            assert lib.pa_decode_set_schedule(mode) == 0
+            assert_close(run_fp16(c, variant, partition=256), want,
+                         what=f"{variant} D={head_dim} schedule={mode}")
+    finally:
+        lib.pa_decode_set_schedule(0)
 
 
 @pytest.mark.parametrize("variant", F16_VARIANTS)
@@ -256,10 +276,13 @@ def test_int8_forced_partition(variant, partition, clen):
 
 
 @pytest.mark.parametrize("variant", I8_VARIANTS)
-@pytest.mark.parametrize("head_dim", [64, 256])
-def test_int8_head_dims(variant, head_dim):
-    c = int8_case(2, make_lens(600, 2), 8, 2, head_dim=head_dim, seed=17)
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
+@pytest.mark.parametrize("num_heads,num_kv_heads", [(8, 2), (32, 1)])
+def test_int8_head_dims(variant, head_dim, num_heads, num_kv_heads):
+    c = int8_case(2, make_lens(600, 2), num_heads, num_kv_heads, head_dim=head_dim, seed=17)
     assert_close(run_int8(c, variant), oracle_int8(c), what=f"{variant} D={head_dim}")
+    assert_close(run_int8(c, variant, partition=128), oracle_int8(c),
+                 what=f"{variant} D={head_dim} P=128")
 
 
 @pytest.mark.parametrize("variant", I8_VARIANTS)
@@ -401,7 +424,8 @@ def test_long_context_element_outliers(variant):
 # ---------------------------------------------------------------- boundary / runtime
 
 def test_capi_direct_call():
-    """The C ABI called through ctypes, workspace owned by the caller."""
+    """The C ABI called through ctypes, counters and workspace owned by the caller;
+    one counter buffer serves both kinds and stays zero after each call."""
     import pa_int8
 
     lib = pa_int8.capi()
@@ -412,22 +436,31 @@ def test_capi_direct_call():
     S, H, D = c["q"].shape
     NB, Hkv = c["k_cache"].shape[:2]
     MB = c["block_table"].shape[1]
+    stream = torch.cuda.current_stream().cuda_stream
+    cb = lib.pa_decode_counter_bytes(S, H, Hkv)
+    counters = torch.full((cb,), 0x5A, dtype=torch.uint8, device=DEV)
+    assert lib.pa_decode_counters_reset(counters.data_ptr(), cb, stream) == 0
     for fn, kind in ((lib.pa_paged_decode_attn_warp, 0), (lib.pa_paged_decode_attn_splitk, 1)):
-        need = lib.pa_decode_workspace_bytes(kind, S, H, D, Hkv, 16, MB, 0, 0)
-        ws = torch.zeros(need + 256, dtype=torch.uint8, device=DEV)
-        base = ws.data_ptr()
-        aligned = (base + 255) // 256 * 256
-        stream = torch.cuda.current_stream().cuda_stream
+        need = lib.pa_decode_workspace_bytes(kind, S, H, D, Hkv, 16, MB, 0, 64)
+        # scratch with arbitrary contents
+        ws = torch.full((need + 256,), 0xFF, dtype=torch.uint8, device=DEV)
+        aligned = (ws.data_ptr() + 255) // 256 * 256
+        out.zero_()
         st = fn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
-                ln.data_ptr(), ctypes.c_float(c["scale"]), 16, S, H, D, Hkv, NB, 8, MB, 0, 0,
-                aligned, need, stream)
+                ln.data_ptr(), ctypes.c_float(c["scale"]), 16, S, H, D, Hkv, NB, 8, MB, 0, 64,
+                counters.data_ptr(), cb, aligned, need, stream)
         assert st == 0, lib.pa_status_string(st)
         torch.cuda.synchronize()
         assert_close(out.float().cpu().numpy(), oracle_fp16(c), what=f"capi kind {kind}")
-        # too-small workspace is refused before any launch
+        assert int(counters.count_nonzero()) == 0
+        # too-small workspace / counters are refused before any launch
         st = fn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
                 ln.data_ptr(), ctypes.c_float(c["scale"]), 16, S, H, D, Hkv, NB, 8, MB, 0, 64,
-                aligned, 16, stream)
+                counters.data_ptr(), cb, aligned, 16, stream)
+        assert st == 5
+        st = fn(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+                ln.data_ptr(), ctypes.c_float(c["scale"]), 16, S, H, D, Hkv, NB, 8, MB, 0, 64,
+                counters.data_ptr(), cb - 256, aligned, need, stream)
         assert st == 5
 
 

@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "pa_mi355x.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("pa_mi355x.h", "pa_mi355x_tuning.h")]
+PROBE_HEADER = os.path.join(ROOT, "cuda-pa-int8_amd", "csrc", "bench", "pa_probe.h")
 
 
 @pytest.fixture(scope="module")
@@ -19,17 +20,19 @@ def lib(built):
     return pa_int8.capi()
 
 
-def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text)))
+def declared_functions(headers=HEADERS):
+    names = set()
+    for h in headers:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol(built):
     lib_path, _ = built
     so = ctypes.CDLL(lib_path)
     names = declared_functions()
-    assert len(names) >= 12
+    assert len(names) >= 16
     missing = [n for n in names if not hasattr(so, n)]
     assert not missing, missing
 
@@ -38,6 +41,18 @@ def test_prototypes_cover_the_header(built):
     from pa_int8 import _loader
 
     assert set(declared_functions()) == set(_loader.PROTOTYPES)
+
+
+def test_probes_live_outside_the_product_library(built):
+    """The benchmark's probes are declared and exported by their own library only."""
+    from pa_int8 import _loader
+
+    probe_names = declared_functions([PROBE_HEADER])
+    assert set(probe_names) == set(_loader.PROBE_PROTOTYPES)
+    product = ctypes.CDLL(built[0])
+    probes = _loader.probe_capi()
+    for n in probe_names:
+        assert hasattr(probes, n) and not hasattr(product, n), n
 
 
 def test_version_and_status_strings(lib):
@@ -61,12 +76,14 @@ def test_validate_block_size_rule(lib, bs, f16_ok, i8_ok):
 
 def test_validate_shape_rules(lib):
     assert lib.pa_validate_decode(0, 2, 8, 128, 2, 10, 16, 4, 4) == 4      # x != 8
-    assert lib.pa_validate_decode(0, 2, 8, 96, 2, 10, 16, 8, 4) == 4       # head_dim not built
+    for d in (72, 120, 160, 192, 512):                                     # head_dim not built
+        assert lib.pa_validate_decode(0, 2, 8, d, 2, 10, 16, 8, 4) == 4
     assert lib.pa_validate_decode(0, 2, 8, 128, 3, 10, 16, 8, 4) == 2      # H % Hkv
     assert lib.pa_validate_decode(0, 2, 8, 128, 2, 0, 16, 8, 4) == 2       # no blocks
     assert lib.pa_validate_decode(0, 0, 8, 128, 2, 0, 16, 8, 0) == 0       # empty batch is fine
-    for d in (64, 128, 256):
-        assert lib.pa_validate_decode(3, 1, 32, d, 1, 1, 16, 8, 1) == 0
+    for d in (64, 80, 96, 112, 128, 256):
+        for kind in range(4):
+            assert lib.pa_validate_decode(kind, 1, 32, d, 1, 1, 16, 8, 1) == 0
 
 
 def test_check_context_lens(lib):
@@ -90,7 +107,12 @@ def test_plan_invariants(lib, s, h, hkv, ctx):
         assert ns.value >= 1 and part.value * ns.value >= ctx
         assert part.value * (ns.value - 1) < ctx
         need = lib.pa_decode_workspace_bytes(kind, s, h, 128, hkv, 16, mb, ctx, 0)
-        assert need % 256 == 0 and need >= lib.pa_decode_counter_bytes(s, h, hkv)
+        assert need % 256 == 0 and need > 0
+    # counters: the 8 claim counters (1 KB), then one arrival counter per
+    # (sequence, kv head, head chunk of <= 16 query heads)
+    chunks = -(-(h // hkv) // 16)
+    units = s * hkv * chunks
+    assert lib.pa_decode_counter_bytes(s, h, hkv) == 1024 + -(-units * 4 // 256) * 256
     # forced partition sizes are rounded up to 64 tokens
     assert lib.pa_decode_plan(0, s, h, 128, hkv, 16, mb, ctx, 100, ctypes.byref(part),
                               ctypes.byref(ns)) == 0
@@ -116,7 +138,10 @@ def test_forced_partition_is_capped(lib):
         lib.pa_decode_set_waves_per_group(0)
 
 
-def test_probe_host_checks(lib):
+def test_probe_host_checks(built):
+    from pa_int8 import _loader
+
+    lib = _loader.probe_capi()
     # rejected before any device access: chunk sizes outside {1, 2, 4k*n} KB
     for chunk in (0, 512, 3072, 6144):
         assert lib.pa_probe_read_chunks(16, 1 << 20, 16, 4, chunk, 16, 64, None) == 2
@@ -133,14 +158,50 @@ def test_waves_override_hook(lib):
         assert lib.pa_decode_set_waves_per_group(w) == 0
 
 
+def test_tuning_hooks_are_per_thread(lib):
+    """A hook set on one thread leaves the plans of other threads alone."""
+    import threading
+
+    part, ns = ctypes.c_int32(), ctypes.c_int32()
+
+    def plan():
+        assert lib.pa_decode_plan(1, 8, 32, 128, 8, 16, 8192, 131072, 100000, ctypes.byref(part),
+                                  ctypes.byref(ns)) == 0
+        return part.value
+
+    base = plan()
+    seen = []
+    t = threading.Thread(target=lambda: (lib.pa_decode_set_waves_per_group(4), seen.append(plan()),
+                                         lib.pa_decode_set_waves_per_group(0)))
+    t.start()
+    t.join()
+    assert seen == [base // 2] and plan() == base
+
+
 def test_decode_rejects_missing_workspace(lib):
-    # host-side refusal before any device access: NULL workspace
-    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, ctypes.c_float(0.1), 16, 2, 8, 128, 2,
-                                       10, 8, 4, 0, 0, None, 0, None)
+    # host-side refusal before any device access: NULL counters or workspace
+    f = ctypes.c_float(0.1)
+    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, f, 16, 2, 8, 128, 2, 10, 8, 4, 0, 0,
+                                       None, 0, None, 0, None)
     assert st == 5
-    st = lib.pa_paged_decode_attn_warp(None, 1, 1, 1, 1, 1, ctypes.c_float(0.1), 16, 2, 8, 128, 2,
-                                       10, 8, 4, 0, 0, None, 0, None)
+    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, f, 16, 2, 8, 128, 2, 10, 8, 4, 0, 0,
+                                       256, 1 << 20, None, 0, None)
+    assert st == 5
+    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, f, 16, 2, 8, 128, 2, 10, 8, 4, 0, 0,
+                                       256, 16, 512, 1 << 20, None)       # counters too small
+    assert st == 5
+    st = lib.pa_paged_decode_attn_warp(1, 1, 1, 1, 1, 1, f, 16, 2, 8, 128, 2, 10, 8, 4, 0, 0,
+                                       260, 1 << 20, 512, 1 << 20, None)  # misaligned counters
+    assert st == 5
+    st = lib.pa_paged_decode_attn_warp(None, 1, 1, 1, 1, 1, f, 16, 2, 8, 128, 2, 10, 8, 4, 0, 0,
+                                       None, 0, None, 0, None)
     assert st == 1
+
+
+def test_counters_reset_host_checks(lib):
+    assert lib.pa_decode_counters_reset(None, 0, None) == 0       # nothing to do
+    assert lib.pa_decode_counters_reset(None, 64, None) == 1
+    assert lib.pa_decode_counters_reset(256, 6, None) == 2        # not whole words
 
 
 def test_quant_write_host_checks(lib):
@@ -215,6 +276,20 @@ def test_extension_exports_reference_op_names(built):
                "paged_decode_attn_splitk", "paged_decode_attn_warp_int8",
                "paged_decode_attn_splitk_int8", "paged_decode_attention"):
         assert callable(getattr(ext, op)), op
+
+
+def test_naive_module_under_its_own_name(built):
+    """The reference builds its naive op as the module paged_attn_naive
+    (kernels/paged_attention_naive.cu:169-172); after loading, both module
+    names import, as the reference's JIT-built modules do."""
+    import importlib
+
+    from pa_int8 import _loader
+
+    naive = _loader.naive_ext()
+    assert callable(naive.paged_decode_attention)
+    assert importlib.import_module("paged_attn_naive") is naive
+    assert importlib.import_module("paged_attn_opt") is _loader.ext()
 
 
 def test_paged_cache_class_host_logic():

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import assert_close
+from _cases import HEAD_DIMS, assert_close
 from oracle import paged_decode_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -227,7 +227,7 @@ def _scattered_slots(rng, T, nb, bs, holes=True):
     return slots
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
 @pytest.mark.parametrize("block_size", [8, 16, 32, 128])
 @pytest.mark.parametrize("num_tokens", [1, 37, 300])
 def test_f16_write_op_matches_oracle(head_dim, block_size, num_tokens):
@@ -251,7 +251,7 @@ def test_f16_write_op_matches_oracle(head_dim, block_size, num_tokens):
         assert np.array_equal(_np(vc).view(np.uint16), ev.view(np.uint16))
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
 @pytest.mark.parametrize("block_size", [16, 64])
 @pytest.mark.parametrize("num_tokens", [1, 45, 512])
 def test_static_int8_write_op_matches_oracle(head_dim, block_size, num_tokens):

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import assert_close, make_lens
+from _cases import HEAD_DIMS, assert_close, make_lens
 from oracle import paged_decode_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -131,14 +131,14 @@ def run_case(T, hkv, d, bs, pattern, seed, kv=None):
                               f"got {g[tuple(bad[0])]} want {e[tuple(bad[0])]}"
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
 @pytest.mark.parametrize("block_size", [16, 32, 64, 128])
 @pytest.mark.parametrize("pattern", ["prefill", "scattered", "padding"])
 def test_quant_write_bitexact(head_dim, block_size, pattern):
     run_case(T=301, hkv=2, d=head_dim, bs=block_size, pattern=pattern, seed=head_dim + block_size)
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim", HEAD_DIMS)
 @pytest.mark.parametrize("pattern", ["prefill", "scattered"])
 def test_quant_write_near_ties(head_dim, pattern):
     """Every element near a rounding tie: the kernel's reciprocal fast path must
