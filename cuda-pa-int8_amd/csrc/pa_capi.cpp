@@ -96,6 +96,7 @@ struct Plan {
   // units; the kernel picks the partition in [pmin, pmax].
   bool sched = false;
   int rows_max = 0;
+  int rows_min = 0;       // rows at the upper partition bound: the least the partials may hold
   int pmin = 0, pmax = 0;
   int pmin_uniform = 0;   // lower bound the kernel uses when all lengths are equal
   bool nt_loads = false;  // non-temporal V-row loads
@@ -186,6 +187,7 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
         ((long long)kSchedGroupsBound * pa::kSchedItemsPerGroup + num_kv_heads - 1) / num_kv_heads;
     const long long by_cap = ((long long)num_seqs * cap + p.pmax - 1) / p.pmax;
     p.rows_max = (int)std::min<long long>(1 << 30, num_seqs + std::max(by_items, by_cap) + 1);
+    p.rows_min = (int)std::min<long long>(1 << 30, num_seqs + by_cap + 1);
   }
   return p;
 }
@@ -218,46 +220,75 @@ WsLayout ws_layout(const Plan& p, int head_dim, int num_seqs) {
   return w;
 }
 
-pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const void* k_cache,
-                          const void* v_cache, const float* k_scales, const float* v_scales,
-                          const int32_t* block_table, const int32_t* context_lens, float scale,
-                          int32_t block_size, int32_t num_seqs, int32_t num_heads,
-                          int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks, int32_t x,
-                          int32_t max_blocks, int32_t max_context_len, int32_t partition_tokens,
-                          void* counters, size_t counter_bytes, void* workspace,
-                          size_t workspace_bytes, pa_stream_t stream) {
-  pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads,
-                                      num_blocks, block_size, x, max_blocks);
-  if (st != PA_OK) return st;
-  if (num_seqs == 0) return PA_OK;
-  if (!out || !q || !k_cache || !v_cache || !block_table || !context_lens) return PA_ERR_NULL_POINTER;
-  if (!is_f16(kind) && (!k_scales || !v_scales)) return PA_ERR_NULL_POINTER;
+// Validates a call and plans it.  `ws_fit` > 0 caps the workspace: the
+// in-kernel schedule's row capacity is lowered until its partials fit (the
+// kernel then doubles its partition when the rows would exceed them), down to
+// the rows it needs at the longest partition; a call that still does not fit
+// gets PA_ERR_SCRATCH_LIMIT.  No device access.
+pa_status_t decode_plan_call(const pa::DecodeCall& c, size_t ws_fit, Plan* plan, WsLayout* layout) {
+  const pa_status_t st = pa_validate_decode(c.kind, c.num_seqs, c.num_heads, c.head_dim,
+                                            c.num_kv_heads, c.num_blocks, c.block_size, c.x,
+                                            c.max_blocks);
+  if (st != PA_OK || c.num_seqs == 0) return st;
+  if (!c.out || !c.q || !c.k_cache || !c.v_cache || !c.block_table || !c.context_lens)
+    return PA_ERR_NULL_POINTER;
+  if (!is_f16(c.kind) && (!c.k_scales || !c.v_scales)) return PA_ERR_NULL_POINTER;
 
-  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
-                           max_blocks, max_context_len, partition_tokens);
+  Plan p = make_plan(c.kind, c.num_seqs, c.num_heads, c.num_kv_heads, c.head_dim, c.block_size,
+                     c.max_blocks, c.max_context_len, c.partition_tokens);
   if (!p.sched) {
     // The grid form launches (sequence, split) items rounded up to groups of 8,
     // times the kv heads and head chunks; a dispatch counts work-items in 32 bits.
-    const long long items = (long long)num_seqs * p.nsplit;
-    const long long groups = (items + 7) / 8 * 8 * num_kv_heads * p.nchunk;
+    const long long items = (long long)c.num_seqs * p.nsplit;
+    const long long groups = (items + 7) / 8 * 8 * c.num_kv_heads * p.nchunk;
     if (groups * p.waves * 64 > 0xFFFFFFFFll) return PA_ERR_BAD_SHAPE;
   }
-  const WsLayout wl = ws_layout(p, head_dim, num_seqs);
+  WsLayout wl = ws_layout(p, c.head_dim, c.num_seqs);
+  if (ws_fit > 0 && wl.total > ws_fit) {
+    if (!p.sched) return PA_ERR_SCRATCH_LIMIT;
+    Plan lo = p;
+    lo.rows_max = p.rows_min;
+    if (ws_layout(lo, c.head_dim, c.num_seqs).total > ws_fit) return PA_ERR_SCRATCH_LIMIT;
+    int a = p.rows_min, b = p.rows_max;   // largest row capacity that fits, in [a, b)
+    while (b - a > 1) {
+      lo.rows_max = a + (b - a) / 2;
+      if (ws_layout(lo, c.head_dim, c.num_seqs).total <= ws_fit) a = lo.rows_max;
+      else b = lo.rows_max;
+    }
+    p.rows_max = a;
+    wl = ws_layout(p, c.head_dim, c.num_seqs);
+  }
+  *plan = p;
+  *layout = wl;
+  return PA_OK;
+}
+
+pa_status_t decode_common(const pa::DecodeCall& c, void* counters, size_t counter_bytes,
+                          void* workspace, size_t workspace_bytes, pa_stream_t stream,
+                          size_t ws_fit) {
+  Plan p;
+  WsLayout wl;
+  const pa_status_t st = decode_plan_call(c, ws_fit, &p, &wl);
+  if (st != PA_OK || c.num_seqs == 0) return st;
   if (!counters || counter_bytes < counter_region(p.units)) return PA_ERR_WORKSPACE;
   if (!workspace || workspace_bytes < wl.total) return PA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0 ||
       reinterpret_cast<uintptr_t>(counters) % kAlign != 0)
     return PA_ERR_WORKSPACE;
+  const pa_decode_kind_t kind = c.kind;
+  void* out = c.out;
+  const int num_seqs = c.num_seqs, num_heads = c.num_heads, head_dim = c.head_dim;
+  const int num_kv_heads = c.num_kv_heads, block_size = c.block_size;
 
   pa::DecodeLaunch l{};
   l.out = out;
-  l.q = q;
-  l.k_cache = k_cache;
-  l.v_cache = v_cache;
-  l.k_scales = k_scales;
-  l.v_scales = v_scales;
-  l.block_table = block_table;
-  l.context_lens = context_lens;
+  l.q = c.q;
+  l.k_cache = c.k_cache;
+  l.v_cache = c.v_cache;
+  l.k_scales = c.k_scales;
+  l.v_scales = c.v_scales;
+  l.block_table = c.block_table;
+  l.context_lens = c.context_lens;
   char* cn = static_cast<char*>(counters);
   l.queue = reinterpret_cast<uint32_t*>(cn);
   l.counters = reinterpret_cast<uint32_t*>(cn + align_up(kQueueBytes));
@@ -292,17 +323,38 @@ pa_status_t decode_common(pa_decode_kind_t kind, void* out, const void* q, const
   sh.nchunk = p.nchunk;
   sh.block_size = block_size;
   sh.bs_log2 = ilog2(block_size);
-  sh.num_blocks = num_blocks;
-  sh.max_blocks = max_blocks;
+  sh.num_blocks = c.num_blocks;
+  sh.max_blocks = c.max_blocks;
   sh.partition = p.partition;
   sh.nsplit = p.nsplit;
   sh.num_items = num_seqs * p.nsplit;
-  sh.scale_log2 = scale * 1.4426950408889634f;
+  sh.scale_log2 = c.scale * 1.4426950408889634f;
 
   return pa::launch_decode(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
 
 }  // namespace
+
+namespace pa {
+
+pa_status_t decode_sizes_capped(const DecodeCall& c, size_t ws_cap, size_t* counter_bytes,
+                                size_t* workspace_bytes) {
+  Plan p;
+  WsLayout wl;
+  const pa_status_t st = decode_plan_call(c, ws_cap, &p, &wl);
+  if (st != PA_OK) return st;
+  *counter_bytes = c.num_seqs == 0 ? 0 : counter_region(p.units);
+  *workspace_bytes = c.num_seqs == 0 ? 0 : wl.total;
+  return PA_OK;
+}
+
+pa_status_t decode_launch_capped(const DecodeCall& c, void* counters, size_t counter_bytes,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return decode_common(c, counters, counter_bytes, workspace, workspace_bytes,
+                       reinterpret_cast<pa_stream_t>(stream), workspace_bytes);
+}
+
+}  // namespace pa
 
 extern "C" {
 
@@ -316,6 +368,8 @@ const char* pa_status_string(pa_status_t s) {
     case PA_ERR_WORKSPACE: return "counters or workspace NULL, misaligned or smaller than required";
     case PA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
     case PA_ERR_EMPTY_CONTEXT: return "context_lens must be >= 1 (empty sequences unsupported)";
+    case PA_ERR_SCRATCH_LIMIT:
+      return "the call needs more device scratch than the no-alloc entry point's static array";
   }
   return "unknown status";
 }
@@ -421,11 +475,12 @@ pa_status_t pa_decode_counters_reset(void* counters, size_t bytes, pa_stream_t s
                    int32_t max_blocks_per_seq, int32_t max_context_len,                         \
                    int32_t partition_tokens, void* counters, size_t counter_bytes,              \
                    void* workspace, size_t workspace_bytes, pa_stream_t stream) {               \
-    return decode_common(KIND, out, q, k_cache, v_cache, nullptr, nullptr, block_table,         \
-                         context_lens, scale, block_size, num_seqs, num_heads, head_dim,        \
-                         num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,      \
-                         partition_tokens, counters, counter_bytes, workspace, workspace_bytes, \
-                         stream);                                                               \
+    const pa::DecodeCall c{KIND,         out,          q,         k_cache,                      \
+                           v_cache,      nullptr,      nullptr,   block_table,                  \
+                           context_lens, scale,        block_size, num_seqs,                    \
+                           num_heads,    head_dim,     num_kv_heads, num_blocks,                \
+                           x,            max_blocks_per_seq, max_context_len, partition_tokens}; \
+    return decode_common(c, counters, counter_bytes, workspace, workspace_bytes, stream, 0);   \
   }
 #define PA_DECODE_ENTRY_I8(NAME, KIND)                                                           \
   pa_status_t NAME(void* out, const void* q, const void* k_cache, const void* v_cache,          \
@@ -436,11 +491,12 @@ pa_status_t pa_decode_counters_reset(void* counters, size_t bytes, pa_stream_t s
                    int32_t max_blocks_per_seq, int32_t max_context_len,                         \
                    int32_t partition_tokens, void* counters, size_t counter_bytes,              \
                    void* workspace, size_t workspace_bytes, pa_stream_t stream) {               \
-    return decode_common(KIND, out, q, k_cache, v_cache, k_scales, v_scales, block_table,       \
-                         context_lens, scale, block_size, num_seqs, num_heads, head_dim,        \
-                         num_kv_heads, num_blocks, x, max_blocks_per_seq, max_context_len,      \
-                         partition_tokens, counters, counter_bytes, workspace, workspace_bytes, \
-                         stream);                                                               \
+    const pa::DecodeCall c{KIND,         out,          q,         k_cache,                      \
+                           v_cache,      k_scales,     v_scales,  block_table,                  \
+                           context_lens, scale,        block_size, num_seqs,                    \
+                           num_heads,    head_dim,     num_kv_heads, num_blocks,                \
+                           x,            max_blocks_per_seq, max_context_len, partition_tokens}; \
+    return decode_common(c, counters, counter_bytes, workspace, workspace_bytes, stream, 0);   \
   }
 
 PA_DECODE_ENTRY_F16(pa_paged_decode_attn_warp, PA_DECODE_WARP_F16)

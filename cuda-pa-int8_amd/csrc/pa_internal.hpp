@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "pa_mi355x.h"
+
 namespace pa {
 
 constexpr int kIterTokens = 64;      // partition granularity (one wave iteration for head_dim <= 128)
@@ -78,6 +80,42 @@ struct DecodeLaunch {
   uint32_t* queue;     // 8 claim counters, zero between launches
   hipStream_t stream;
 };
+
+// One decode call's arguments as the C ABI passes them (pa_mi355x.h), minus
+// the device memory and the stream.
+struct DecodeCall {
+  pa_decode_kind_t kind;
+  void* out;
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const float* k_scales;
+  const float* v_scales;
+  const int32_t* block_table;
+  const int32_t* context_lens;
+  float scale;
+  int32_t block_size;
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t num_kv_heads;
+  int32_t num_blocks;
+  int32_t x;
+  int32_t max_blocks;
+  int32_t max_context_len;
+  int32_t partition_tokens;
+};
+
+// Defined in pa_capi.cpp, for the no-alloc entry point (pa_noalloc.hip).
+// decode_sizes_capped validates and plans `c` with at most `ws_cap` bytes of
+// workspace (the in-kernel schedule's row capacity is lowered to fit) and
+// returns the counter and workspace bytes the call then uses, or
+// PA_ERR_SCRATCH_LIMIT; no device access.  decode_launch_capped does the
+// same and launches.
+pa_status_t decode_sizes_capped(const DecodeCall& c, size_t ws_cap, size_t* counter_bytes,
+                                size_t* workspace_bytes);
+pa_status_t decode_launch_capped(const DecodeCall& c, void* counters, size_t counter_bytes,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // Head dims the library is built for.  The decode kernels are instantiated
 // once per head_dim from pa_decode_inst.hip (compiled with -DPA_HEAD_DIM=D);

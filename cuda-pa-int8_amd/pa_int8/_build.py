@@ -41,6 +41,7 @@ HIP_SOURCES = [
     "pa_quant.hip",
     "pa_cache_write.hip",
     "pa_fill.hip",
+    "pa_noalloc.hip",
 ]
 HOST_SOURCES = ["pa_capi.cpp"]
 PROBE_SOURCES = ["bench/pa_probe.hip"]

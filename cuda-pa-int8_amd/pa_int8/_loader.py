@@ -93,6 +93,8 @@ PROTOTYPES = {
     "pa_paged_decode_attn_splitk": (ctypes.c_int, _DECODE_F16_ARGS),
     "pa_paged_decode_attn_warp_int8": (ctypes.c_int, _DECODE_I8_ARGS),
     "pa_paged_decode_attn_splitk_int8": (ctypes.c_int, _DECODE_I8_ARGS),
+    "pa_paged_decode_attn_noalloc": (ctypes.c_int, [ctypes.c_int] + [_p] * 8 + _DECODE_TAIL[:11]
+                                     + [_p]),
     "pa_reshape_and_cache_int8": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32,
                                                  _i32, _p, _p, _p, _p, _i32, _i32, _i32, _p]),
     "pa_reshape_and_cache_int8_static": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p,

@@ -63,7 +63,8 @@ typedef enum pa_status {
   PA_ERR_UNSUPPORTED = 4,      /* head_dim / x not built into this library */
   PA_ERR_WORKSPACE = 5,        /* counters / workspace NULL, misaligned or too small */
   PA_ERR_LAUNCH = 6,           /* the HIP runtime refused the launch */
-  PA_ERR_EMPTY_CONTEXT = 7     /* a context length < 1 (host-side check) */
+  PA_ERR_EMPTY_CONTEXT = 7,    /* a context length < 1 (host-side check) */
+  PA_ERR_SCRATCH_LIMIT = 8     /* beyond the no-alloc entry point's static scratch */
 } pa_status_t;
 
 /* Decode kinds for the planning / workspace queries. */
@@ -167,6 +168,32 @@ pa_status_t pa_paged_decode_attn_splitk_int8(
     int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
     int32_t partition_tokens, void* counters, size_t counter_bytes, void* workspace,
     size_t workspace_bytes, pa_stream_t stream);
+
+/* Decode that allocates nothing.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The same call as
+ * the decode entry point of `kind` (pa_paged_decode_attn_warp, _splitk,
+ * _warp_int8 or _splitk_int8; k_scales / v_scales are ignored for the FP16
+ * kinds), minus the counters and workspace: those live in one static device
+ * array of PA_NOALLOC_SCRATCH_BYTES per GPU (the first
+ * PA_NOALLOC_COUNTER_BYTES hold the counters, the rest the split partials),
+ * which the library keeps until the process ends.  Each call clears the
+ * counters it uses with a fill kernel on `stream` before the decode; it calls
+ * no hipMalloc, hipFree or allocating library routine.  A call whose counters
+ * or partials do not fit gets PA_ERR_SCRATCH_LIMIT before anything is
+ * launched (the in-kernel schedule's split capacity shrinks to fit first, so
+ * only very large batches are refused).  Every call on a GPU shares that
+ * GPU's array: two calls that may overlap on one GPU (different streams, or
+ * concurrently replayed graphs) race and give wrong results. */
+#define PA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define PA_NOALLOC_COUNTER_BYTES ((size_t)1 << 20)
+pa_status_t pa_paged_decode_attn_noalloc(
+    pa_decode_kind_t kind, void* out, const void* q, const void* k_cache, const void* v_cache,
+    const float* k_scales, const float* v_scales,
+    const int32_t* block_table, const int32_t* context_lens, float scale, int32_t block_size,
+    int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t num_kv_heads,
+    int32_t num_blocks, int32_t x, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, pa_stream_t stream);
 
 /* Per-token INT8 quantize + paged-cache write.  NEW API: the reference has
  * no kernel for it; its semantics are those of quantize_per_token

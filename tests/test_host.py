@@ -57,7 +57,7 @@ def test_probes_live_outside_the_product_library(built):
 
 def test_version_and_status_strings(lib):
     assert b"gfx950" in lib.pa_version()
-    for code in range(8):
+    for code in range(9):
         assert lib.pa_status_string(code)
     assert lib.pa_status_string(99) == b"unknown status"
 
