@@ -11,6 +11,8 @@ Yevsquant/cuda-PA-INT8) in vectorised numpy:
 * ``paged_decode_attention``     tests/paged_decode_attn.py:4-49
 * ``build_paged_kv_cache``       tests/paged_decode_attn.py:52-101
 * ``quantize_per_token``         tests/paged_decode_attn.py:106-112
+* ``quantize_per_token_bf16``    the same on bfloat16 input (bit patterns;
+                                 numpy has no bfloat16)
 * ``quantize_per_tensor``        tests/paged_decode_attn.py:115-121
 * ``build_paged_kv_cache_int8``  tests/paged_decode_attn.py:124-199
 * ``dequantize_kv``              tests/paged_decode_attn.py:202-216
@@ -53,6 +55,9 @@ __all__ = [
     "dense_attention",
     "build_paged_kv_cache",
     "quantize_per_token",
+    "quantize_per_token_bf16",
+    "bf16_bits_to_f32",
+    "f32_to_bf16_bits",
     "quantize_per_tensor",
     "build_paged_kv_cache_int8",
     "dequantize_kv",
@@ -246,6 +251,36 @@ def quantize_per_token(x, axis=-1):
     scale = _scale_from_amax(amax)
     q = _quantize_with_scale(x, scale)
     return q, np.squeeze(scale, axis=axis)
+
+
+def bf16_bits_to_f32(bits):
+    """bfloat16 bit patterns (uint16) -> float32 values (exact)."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)
+    return b.view(np.float32)
+
+
+def f32_to_bf16_bits(x):
+    """float32 -> bfloat16 bit patterns, round to nearest even (NaN stays NaN)."""
+    b = np.asarray(x, dtype=np.float32).view(np.uint32)
+    rounded = (b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    return np.where(nan, (b >> np.uint32(16)) | np.uint32(0x40), rounded).astype(np.uint16)
+
+
+def quantize_per_token_bf16(bits, axis=-1):
+    """quantize_per_token (tests/paged_decode_attn.py:106-112) on a bfloat16
+    tensor given as bit patterns.  ``amax``, ``clamp_min(1e-8)`` and the
+    division by 127 happen in bfloat16: torch widens to float32, computes, and
+    rounds once to bfloat16 (for the quotient a correctly rounded float32
+    division rounded again to bfloat16, which equals one rounding since
+    24 >= 2 * 8 + 2); 1e-8 itself becomes the nearest bfloat16 value."""
+    x = bf16_bits_to_f32(bits)
+    amax = np.abs(x).max(axis=axis, keepdims=True)
+    lo = bf16_bits_to_f32(f32_to_bf16_bits(np.float32(1e-8)))
+    a = np.where(np.isnan(amax), amax, np.maximum(amax, lo))
+    scale = bf16_bits_to_f32(f32_to_bf16_bits(a / np.float32(127.0)))
+    q = _quantize_with_scale(x, scale)
+    return q, np.squeeze(scale, axis=axis).astype(np.float32)
 
 
 def quantize_per_tensor(x):

@@ -79,12 +79,31 @@ def oracle_int8(c):
 
 
 def assert_close(out, expect, atol=ATOL, rtol=RTOL, what=""):
+    """Elementwise |out - expect| <= atol + rtol * |expect|.  Returns the
+    headroom ratio max(|out - expect| / (atol + rtol * |expect|)): 1.0 is the
+    edge of the tolerance, small values mean a wide margin."""
     out = np.asarray(out, dtype=np.float32)
     expect = np.asarray(expect, dtype=np.float32)
     err = np.abs(out - expect)
-    bad = err > atol + rtol * np.abs(expect)
+    bound = atol + rtol * np.abs(expect)
+    bad = err > bound
     if bad.any():
         i = np.unravel_index(np.argmax(err - rtol * np.abs(expect)), err.shape)
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{bad.size} elements outside atol={atol} rtol={rtol}; "
             f"worst at {i}: got {out[i]}, want {expect[i]}, max|err|={err.max():.3e}")
+    return float((err / bound).max()) if err.size else 0.0
+
+
+def record_headroom(config, what, ratio, **extra):
+    """Appends one line of JSON (config, case, headroom ratio) to the file named
+    by PA_PARITY_LOG, when it is set; the full-size parity tests call it."""
+    import json
+    import os
+
+    path = os.environ.get("PA_PARITY_LOG")
+    line = dict(config=config, case=what, headroom=round(ratio, 4), **extra)
+    print("[parity]", json.dumps(line), flush=True)
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(line) + "\n")

@@ -19,7 +19,8 @@ import pytest
 import torch
 
 from _cases import (ATOL, CONTEXT_LENS, GQA, HEAD_DIMS, LONG_CONTEXT_LENS, NUM_SEQS, RTOL,
-                    assert_close, fp16_case, int8_case, make_lens, oracle_fp16, oracle_int8)
+                    assert_close, fp16_case, int8_case, make_lens, oracle_fp16, oracle_int8,
+                    record_headroom)
 
 pytestmark = pytest.mark.gpu
 
@@ -180,7 +181,9 @@ def test_fp16_qwen_config_full_size():
     c = fp16_case(32, np.full(32, 4096, dtype=np.int32), 12, 2, seed=2)
     ref = oracle_fp16(c)
     for variant in F16_VARIANTS:
-        assert_close(run_fp16(c, variant), ref, what=variant)
+        ratio = assert_close(run_fp16(c, variant), ref, what=variant)
+        record_headroom("cfg2", f"{variant} 32 x 4096 12/2, all sequences", ratio,
+                        variant=variant, seqs_checked=32)
 
 
 @pytest.mark.parametrize("variant", F16_VARIANTS)
@@ -418,7 +421,9 @@ def test_long_context_element_outliers(variant):
                                                            rng=rng)
         c.update(k_cache8=kc, v_cache8=vc, k_scales=ks, v_scales=vs, block_table8=bt)
         out, want = run_int8(c, variant), oracle_int8(c)
-    assert_close(out, want, what=f"{variant} 32k outliers")
+    ratio = assert_close(out, want, what=f"{variant} 32k outliers")
+    record_headroom("cfg4", f"{variant} 2 x 32768 32/8 outliers (numpy-drawn)", ratio,
+                    variant=variant, seqs_checked=2)
 
 
 # ---------------------------------------------------------------- boundary / runtime

@@ -151,6 +151,47 @@ def test_quant_per_token_matches_reference_golden_fp32():
     assert np.array_equal(s.view(np.uint32), z["s32"].view(np.uint32))
 
 
+def test_quant_per_token_matches_reference_golden_nonfinite():
+    """Rows holding NaN or +-inf: amax propagates them into the scale (NaN or
+    inf) and every element converts to 0 (x / inf = 0, NaN -> 0)."""
+    z = _golden()
+    q, s = ref.quantize_per_token(z["xnf"], axis=-1)
+    assert np.array_equal(q, z["qnf"])
+    assert np.array_equal(np.isnan(s), np.isnan(z["snf"]))
+    fin = ~np.isnan(z["snf"])
+    assert np.array_equal(s[fin], z["snf"][fin])
+    assert not q.any() and np.isnan(z["snf"]).any() and np.isinf(z["snf"]).any()
+
+
+def test_quant_per_token_matches_reference_golden_bf16():
+    z = _golden()
+    q, s = ref.quantize_per_token_bf16(z["xb16_bits"], axis=-1)
+    assert np.array_equal(q, z["qb16"])
+    fin = ~np.isnan(z["sb16"])
+    assert np.array_equal(np.isnan(s), ~fin)
+    assert np.array_equal(s[fin].view(np.uint32), z["sb16"][fin].view(np.uint32))
+
+
+def test_bf16_rounding_helpers():
+    """f32 -> bf16 bit rounding agrees with torch's conversion on every bf16
+    neighbourhood we can name: exact values, midpoints (ties to even), and
+    random floats; NaN stays NaN."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    base = rng.integers(0, 1 << 16, size=4096, dtype=np.uint32).astype(np.uint16)
+    f = ref.bf16_bits_to_f32(base)
+    f = f[np.isfinite(f)]
+    mids = (f.view(np.uint32) + np.uint32(0x8000)).view(np.float32)     # exact midpoints
+    rnd = rng.standard_normal(4096).astype(np.float32) * np.float32(1e3)
+    for x in (f, mids[np.isfinite(mids)], rnd, np.array([np.nan, np.inf, -np.inf], np.float32)):
+        want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        got = ref.f32_to_bf16_bits(x)
+        nan = np.isnan(x)
+        assert np.array_equal(got[~nan], want[~nan])
+        assert np.isnan(ref.bf16_bits_to_f32(got[nan])).all()
+
+
 def test_quant_per_tensor_matches_reference_golden():
     z = _golden()
     q, s = ref.quantize_per_tensor(z["xt"])

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import HEAD_DIMS, assert_close, make_lens
+from _cases import HEAD_DIMS, assert_close, make_lens, record_headroom
 from oracle import paged_decode_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -218,4 +218,6 @@ def test_quant_write_full_size_then_decode():
     kd, vd = ref.dequantize_kv(kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
                                vs.cpu().numpy())
     want = ref.paged_decode_attention(q[:4], kd, vd, bt[:4], lens[:4], scale=1.0 / np.sqrt(d))
-    assert_close(out[:4].float().cpu().numpy(), want, what="decode after write")
+    ratio = assert_close(out[:4].float().cpu().numpy(), want, what="decode after write")
+    record_headroom("cfg3", "warp_int8 64 x 8192 12/2 over the kernel-written cache", ratio,
+                    variant="warp_int8", seqs_checked=4)
