@@ -38,7 +38,30 @@ for _p in (ROOT, PKG_ROOT):
 
 METRIC = "decode µs + achieved HBM GB/s (% of peak), FP16 vs INT8 KV, GQA 12/2 d128"
 MALL_BYTES = 256 << 20
-ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "dense", "e2e", "ceiling"]
+ALL_CONFIGS = ["cfg2", "cfg1", "cfg3", "cfg3w", "cfg4", "cfg5", "refshapes", "dense", "e2e",
+               "ceiling"]
+
+# The reference's published A100 rows (head_dim 128, block_size 16, fp16 q/K/V
+# ~ N(0,1)), measured here at the same shapes: (batch, ctx, q heads, kv heads,
+# variant, A100 us, source under the reference checkout).
+REF_SHAPES = [
+    (1, 4096, 8, 8, "splitk", 86.0, "report/kernel_optimization.md:231"),
+    (32, 4096, 8, 8, "splitk", 403.0, "report/kernel_optimization.md:257"),
+    (64, 4096, 8, 8, "warp", 674.7, "report/kernel_optimization.md:269"),
+    (64, 4096, 8, 8, "splitk", 699.8, "report/kernel_optimization.md:270"),
+    (64, 4096, 8, 1, "warp", 458.0, "report/kernel_optimization.md:529"),
+    (64, 4096, 8, 1, "splitk", 398.1, "report/kernel_optimization.md:530"),
+    (32, 4096, 16, 4, "warp", 521.7, "report/kernel_optimization.md:776"),
+    (32, 4096, 16, 4, "splitk", 415.4, "report/kernel_optimization.md:777"),
+    (32, 2048, 8, 8, "warp", 277.7, "report/int8_quant.md:26"),
+    (32, 2048, 8, 8, "splitk", 254.8, "report/int8_quant.md:27"),
+    (32, 2048, 8, 8, "warp_int8", 269.0, "report/int8_quant.md:28"),
+    (32, 2048, 8, 8, "splitk_int8", 199.6, "report/int8_quant.md:29"),
+    (8, 4096, 8, 1, "splitk", 102.6, "report/int8_quant.md:36"),
+    (8, 4096, 8, 1, "splitk_int8", 104.9, "report/int8_quant.md:38"),
+    (32, 4096, 16, 4, "splitk", 438.6, "report/int8_quant.md:45"),
+    (32, 4096, 16, 4, "splitk_int8", 393.6, "report/int8_quant.md:47"),
+]
 
 
 def log(*a):
@@ -186,6 +209,51 @@ def decode_steps(torch, case, variant, partition=0):
     return fns, out
 
 
+def dense_reference(torch, case, seq):
+    """fp32 dense attention of one sequence in torch on the device: its K/V
+    gathered from the first cache copy through the block table (INT8 values
+    times their scales), softmax(scale * K q) V per query head."""
+    kc, vc, ks, vs = case["caches"][0]
+    bs, n = case["bs"], case["lens"][seq]
+    nblk = (n + bs - 1) // bs
+    ids = case["bt"][seq, :nblk].long()
+    hkv, d = kc.shape[1], case["head_dim"]
+    k = kc[ids].permute(0, 3, 1, 2, 4).reshape(nblk * bs, hkv, d).float()   # [t, Hkv, D]
+    v = vc[ids].permute(0, 3, 1, 2).reshape(nblk * bs, hkv, d).float()
+    if ks is not None:
+        k = k * ks[ids].permute(0, 2, 1).reshape(nblk * bs, hkv, 1)
+        v = v * vs[ids].permute(0, 2, 1).reshape(nblk * bs, hkv, 1)
+    k, v = k[:n].permute(1, 2, 0).contiguous(), v[:n].permute(1, 0, 2).contiguous()
+    q = case["q"][seq].float().view(hkv, -1, d)                              # [Hkv, G, D]
+    p = torch.softmax(torch.bmm(q, k) * case["scale"], dim=-1)               # [Hkv, G, t]
+    return torch.bmm(p, v).reshape(-1, d)                                   # [H, D]
+
+
+def gate(torch, case, fns, out, seqs, atol=2e-3, rtol=1e-2):
+    """The correctness gate before timing (as bench_paged_decode.py:180-188 checks
+    every variant first): one call of the timed step, its outputs for `seqs`
+    against dense torch attention in fp32.  Returns {ok, headroom, seqs}."""
+    fns[0]()
+    torch.cuda.synchronize()
+    worst = 0.0
+    for s in seqs:
+        want = dense_reference(torch, case, s)
+        err = (out[s].float() - want).abs()
+        worst = max(worst, float((err / (atol + rtol * want.abs())).max()))
+    return dict(ok=bool(worst <= 1.0), headroom=round(worst, 4), seqs_checked=len(seqs),
+                tolerance=f"atol {atol} rtol {rtol}, fp32 dense torch attention")
+
+
+def gate_seqs(lens, n=6):
+    """Sequences the gate checks: the first, the last, the longest, the shortest
+    and a few between."""
+    S = len(lens)
+    picks = {0, S - 1, int(max(range(S), key=lambda i: lens[i])),
+             int(min(range(S), key=lambda i: lens[i]))}
+    picks |= {i * S // n for i in range(n)}
+    return sorted(picks)
+
+
 # --------------------------------------------------------------------------- configs
 
 def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0, outliers=False,
@@ -196,7 +264,10 @@ def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0,
     per_copy = metrics.decode_kv_bytes(lens, hkv, d, 1 if int8 else 2)
     case = make_case(torch, lens, h, hkv, d, 16, "cuda", seed, int8, outliers,
                      copies_for(per_copy))
-    fns, _ = decode_steps(torch, case, variant, partition)
+    fns, out = decode_steps(torch, case, variant, partition)
+    checked = gate(torch, case, fns, out, gate_seqs(lens, 2 if sum(lens) > 2 ** 20 else 6))
+    if not checked["ok"]:
+        log(f"[bench] GATE FAILED {name} {variant}: headroom {checked['headroom']} > 1")
     if eager_only:
         for i in range(warmup):
             fns[i % len(fns)]()
@@ -215,7 +286,7 @@ def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0,
                                  / (ms * 1e-3) / 1e9, 1),
                seqs=len(lens), heads=f"{h}/{hkv}", head_dim=d, total_tokens=int(sum(lens)),
                partition_tokens=part, splits=ns, cache_copies=len(case["caches"]),
-               steps=steps)
+               steps=steps, ok=checked["ok"], gate=checked)
     if eager:
         res["eager_us"] = round(time_eager(torch, fns, steps) * 1e3, 2)
     del case, fns
@@ -252,13 +323,36 @@ def run_quant_write(torch, steps, warmup, seed=0):
     def mk(kc, vc, ks, vs):
         return lambda: pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots)
 
+    # gate: 4096 sampled tokens against torch's own quantize_per_token on the
+    # device (tests/paged_decode_attn.py:106-112), bytes and scale bits
+    mk(*dests[0])()
+    torch.cuda.synchronize()
+    pick = torch.randperm(T, device=dev, generator=gen)[:4096]
+    kc, vc, ks, vs = dests[0]
+    blk, off = slots[pick] // bs, slots[pick] % bs
+    ok = True
+    for x, cache, sc, is_v in ((k, kc, ks, False), (v, vc, vs, True)):
+        xs = x[pick]                                                     # [n, Hkv, D] fp16
+        amax = xs.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8)
+        want_s = (amax / 127.0).to(torch.float32)
+        want_q = torch.round(xs.to(torch.float32) / want_s).clamp(-127, 127).to(torch.int8)
+        got_q = cache[blk].permute(0, 1, 3, 2) if is_v else \
+            cache[blk].permute(0, 1, 3, 2, 4).reshape(len(pick), hkv, bs, d)
+        got_q = got_q[torch.arange(len(pick), device=dev), :, off]       # [n, Hkv, D]
+        got_s = sc[blk, :, off]
+        ok = ok and bool(torch.equal(got_q, want_q)) and bool(
+            torch.equal(got_s.view(torch.int32), want_s.squeeze(-1).view(torch.int32)))
+    if not ok:
+        log("[bench] GATE FAILED cfg3w quant_write")
     ms = time_steps(torch, [mk(*dd) for dd in dests], steps, warmup, 3)
     nbytes = metrics.quant_write_bytes(T, hkv, d)
     res = dict(us=round(ms * 1e3, 2), algo_bytes=nbytes, gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
                frac_peak=round(nbytes / (ms * 1e-3) / 1e9 / metrics.MI355X_HBM_PEAK_GBS, 4),
                tokens=T, kv_heads=hkv, head_dim=d,
                slot_pattern="per-sequence block runs (prefill), block ids randomly permuted",
-               destination_copies=len(dests), steps=steps)
+               destination_copies=len(dests), steps=steps, ok=ok,
+               gate="4096 sampled tokens: int8 bytes and scale bits equal torch's "
+                    "quantize_per_token on the device")
     log(f"[bench] cfg3w quant_write: {res['us']} us, {res['gbs']} GB/s")
     del k, v, dests
     torch.cuda.empty_cache()
@@ -452,6 +546,18 @@ def run_configs(torch, names, steps, warmup):
         out["cfg5_lens"] = dict(n=256, median=int(np.median(lens)), mean=float(np.mean(lens)),
                                 max=int(max(lens)), sigma=1.0,
                                 distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
+    if "refshapes" in names:
+        rows = []
+        for b, ctx, h, hkv, variant, a100_us, src in REF_SHAPES:
+            r = run_decode_cfg(torch, f"ref b{b} ctx{ctx} {h}/{hkv}", [ctx] * b, h, hkv, 128,
+                               variant, steps_for(max(5, ctx * b * hkv // 50_000), steps), warmup)
+            r.update(a100_us=a100_us, a100_source=src,
+                     a100_over_mi355x_latency=round(a100_us / r["us"], 2))
+            rows.append(r)
+        out["reference_shapes"] = dict(
+            rows=rows, note="the reference's published A100-SXM4-80GB rows (1555 GB/s peak) at "
+                            "the same shapes; kv_only_gbs counts K+V read once, as the "
+                            "reference's GB/s does (bench_paged_decode.py:148-152)")
     if "e2e" in names:
         out["e2e_qwen_bridge"] = run_e2e_bridge(torch)
     if "dense" in names:
@@ -553,16 +659,21 @@ def cpu_baseline(seconds):
     """The numpy oracle on config-2-shaped sequences, for a bounded time."""
     import numpy as np
 
+    from threadpoolctl import threadpool_limits
+
     from oracle import paged_decode_ref as ref
     from pa_int8 import metrics
 
-    try:
-        from threadpoolctl import threadpool_info
+    # the host threads this process may use: its CPU affinity, capped by the
+    # OMP_NUM_THREADS the box sets (its CPU share)
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    with threadpool_limits(limits=threads, user_api="blas"):
+        return _cpu_baseline_timed(seconds, threads, np, ref, metrics)
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()
-                       if i.get("user_api") == "blas"] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
+
+def _cpu_baseline_timed(seconds, threads, np, ref, metrics):
     rng = np.random.default_rng(0)
     n_seq, ctx, h, hkv, d = 2, 4096, 12, 2, 128
     lens = np.full(n_seq, ctx, np.int32)
@@ -588,12 +699,22 @@ def cpu_baseline(seconds):
                         f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32), "
                         f"{n_seq} per call, median of {len(calls)} calls after one warm-up "
                         f"({dt:.1f} s); {seq_ms:.2f} ms per sequence, "
-                        f"{seq_ms * 32:.1f} ms per 32-sequence step"),
+                        f"{seq_ms * 32:.1f} ms per 32-sequence step; BLAS limited to "
+                        f"{threads} threads, the gather and widening run on one"),
                 host_cpus=os.cpu_count(), cpu_model=_cpu_model())
 
 
 def _cpu_model():
-    """The host CPU's model name (Linux /proc/cpuinfo), or None."""
+    """The host CPU's model name (lscpu, else /proc/cpuinfo), or None."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:

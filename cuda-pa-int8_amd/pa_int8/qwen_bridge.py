@@ -1,40 +1,48 @@
-"""Qwen2 decode-step attention through the paged kernels (transformers bridge).
+"""Qwen2 decode-step attention on the paged kernels: a transformers bridge.
 
-Counterpart of benchmarks/int8_bridge/qwen_paged_attn.py:1-164.  A
-transformers ``AttentionInterface`` function replaces only the attention math
-(q/k/v projections, RoPE and o_proj stay in the model; the interface is called
-after RoPE, before the GQA repeat):
+Behaviour of benchmarks/int8_bridge/qwen_paged_attn.py:1-164 -- the same
+interface name, batch 1, a prompt chunk written into the active
+``PagedKVCache`` and attended causally in full precision, every one-token
+step appended to the cache and answered by the split-K decode kernel over it
+-- built around one object instead of module state and parallel loops:
 
-* a prompt chunk (q_len > 1) is written into the active ``PagedKVCache``
-  (quantized for the INT8 variants) and its output is full-precision causal
-  attention over the chunk (:47-55);
-* a decode step (q_len == 1) appends the token's K/V to the cache and takes its
-  output from the split-K decode kernel, FP16 or INT8 (:57-71).
-
-Batch 1, one sequence; the model runs with ``use_cache=False`` and explicit
-``position_ids`` so the interface only ever sees the current chunk
-(:11-13).  The active cache is module state set per generation call.
+* ``DecodeSession(model, cache)`` owns one pass over one sequence.  Entering
+  it binds the cache to the attention interface through a context variable,
+  so a bridged model and a reference model (or two threads) never see each
+  other's cache.
+* ``DecodeSession.step(ids)`` is the only place the model is called: it feeds
+  ``ids`` at the next positions (explicit ``position_ids`` and
+  ``use_cache=False``, so attention only ever receives the new chunk) and
+  returns the last position's logits.
+* Greedy generation and teacher forcing are two token-picking policies over
+  one loop (``_run``): token i is picked from the logits that precede it and
+  fed as the next step.  Teacher forcing skips the forward of its last token,
+  whose logits nobody reads, and reads the log-probabilities back once at the
+  end instead of once per token.
+* A decode step calls the kernel through the no-sync entry: the cache knows
+  its length on the host, so no ``context_lens.min()`` device-to-host copy is
+  made per layer (the reference's op makes one).
 """
 
 from __future__ import annotations
 
+import contextvars
+import math
 import time
 
 import torch
 
-from .registry import VARIANTS, VARIANTS_INT8
+from . import registry
 
-ATTN_NAME = "paged_int8_bridge"          # name of qwen_paged_attn.py:28
+ATTN_NAME = "paged_int8_bridge"          # the interface name of qwen_paged_attn.py:28
 REFERENCE_ATTN_NAME = "pa_fp32_reference"
 
-_active = {"cache": None}
+_SESSION: contextvars.ContextVar = contextvars.ContextVar("pa_int8_decode_session",
+                                                          default=None)
 _registered = set()
 
 
-def set_active_cache(cache):
-    """The PagedKVCache the interface writes to and reads from (:33-35)."""
-    _active["cache"] = cache
-
+# --------------------------------------------------------------------------- attention math
 
 def _causal_fp32(query, key, value, scaling):
     """Causal attention in fp32 over contiguous operands, GQA by repetition.
@@ -70,39 +78,85 @@ def _prefill_attention(query, key, value, scaling):
         return _causal_fp32(query, key, value, scaling)
 
 
+# --------------------------------------------------------------------------- session
+
+class DecodeSession:
+    """One pass of `model` over one sequence with its attention on `cache`.
+
+    Use as a context manager; ``model`` may be None when only the attention
+    interface is driven (``set_active_cache``)."""
+
+    def __init__(self, model, cache):
+        self.model = model
+        self.cache = cache
+        self.position = 0
+        self._token = None
+        if getattr(cache, "is_int8", False):
+            self._kernel = "splitk_int8"
+        else:
+            self._kernel = "splitk"
+
+    def __enter__(self):
+        self.cache.reset()
+        self.position = 0
+        self._token = _SESSION.set(self)
+        return self
+
+    def __exit__(self, *exc):
+        _SESSION.reset(self._token)
+        self._token = None
+        return False
+
+    @torch.no_grad()
+    def step(self, ids):
+        """Feeds `ids` ([1, n]) at the next n positions; returns the logits of
+        the last one ([1, vocab])."""
+        n = ids.shape[1]
+        pos = torch.arange(self.position, self.position + n, device=ids.device).unsqueeze(0)
+        logits = self.model(input_ids=ids, position_ids=pos, use_cache=False).logits[:, -1, :]
+        self.position += n
+        return logits
+
+    def attend(self, layer, query, key, value, scaling):
+        """The interface's work for one layer: query [1, H, n, D] and key/value
+        [1, Hkv, n, D] after RoPE.  Returns [1, n, H, D]."""
+        b, h, n, d = query.shape
+        if b != 1:
+            raise RuntimeError("the paged bridge decodes one sequence (batch 1)")
+        if scaling is None:
+            scaling = d ** -0.5
+        k_tok = key[0].permute(1, 0, 2)                  # [n, Hkv, D], one row per position
+        v_tok = value[0].permute(1, 0, 2)
+        if n > 1:
+            self.cache.prefill(layer, k_tok.contiguous(), v_tok.contiguous())
+            return _prefill_attention(query, key, value, scaling).transpose(1, 2).contiguous()
+        self.cache.decode_append(layer, k_tok[0], v_tok[0])
+        c = self.cache
+        q = query.reshape(1, h, d).to(torch.float16)
+        out = torch.empty_like(q)
+        scales = dict(k_scales=c.k_scales[layer], v_scales=c.v_scales[layer]) if c.is_int8 else {}
+        registry.decode(self._kernel, out, q, c.k_cache[layer], c.v_cache[layer], c.block_table,
+                        c.context_lens(layer), scaling, c.block_size, check=False, **scales)
+        return out.view(1, 1, h, d).to(query.dtype)
+
+
+def set_active_cache(cache):
+    """Binds `cache` to the attention interface in the current context without
+    a model (the reference's module-level switch, qwen_paged_attn.py:33-35);
+    None unbinds.  ``DecodeSession`` does this for a pass of a model."""
+    _SESSION.set(DecodeSession(None, cache) if cache is not None else None)
+
+
 def paged_bridge_attention(module, query, key, value, attention_mask, scaling=None,
                            dropout=0.0, **kwargs):
-    """Attention interface (shapes as transformers passes them):
-    query [1, H, q_len, D], key/value [1, Hkv, q_len, D] (post-RoPE).  Returns
+    """transformers AttentionInterface function of ``ATTN_NAME``: the active
+    session's cache takes the chunk's K/V and answers the query.  Returns
     ``(out [1, q_len, H, D], None)``."""
-    cache = _active["cache"]
-    if cache is None:
-        raise RuntimeError("no active PagedKVCache: call set_active_cache() first")
-    b, h, q_len, d = query.shape
-    if b != 1:
-        raise RuntimeError("the paged bridge decodes one sequence (batch 1)")
-    if scaling is None:
-        scaling = d ** -0.5
-    layer = module.layer_idx
-
-    if q_len > 1:
-        cache.prefill(layer, key[0].transpose(0, 1).contiguous(),
-                      value[0].transpose(0, 1).contiguous())
-        out = _prefill_attention(query, key, value, scaling)
-        return out.transpose(1, 2).contiguous(), None
-
-    cache.decode_append(layer, key[0, :, 0, :], value[0, :, 0, :])
-    q = query[0].transpose(0, 1).contiguous().to(torch.float16)   # [1, H, D]
-    out = torch.empty_like(q)
-    ctx = cache.context_lens(layer)
-    if cache.is_int8:
-        VARIANTS_INT8["splitk_int8"](out, q, cache.k_cache[layer], cache.v_cache[layer],
-                                     cache.k_scales[layer], cache.v_scales[layer],
-                                     cache.block_table, ctx, scaling, cache.block_size)
-    else:
-        VARIANTS["splitk"](out, q, cache.k_cache[layer], cache.v_cache[layer],
-                           cache.block_table, ctx, scaling, cache.block_size)
-    return out.unsqueeze(1).to(query.dtype), None
+    session = _SESSION.get()
+    if session is None:
+        raise RuntimeError("no active PagedKVCache: enter a DecodeSession or call "
+                           "set_active_cache() first")
+    return session.attend(module.layer_idx, query, key, value, scaling), None
 
 
 def reference_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
@@ -116,8 +170,8 @@ def reference_attention(module, query, key, value, attention_mask, scaling=None,
 
 
 def register():
-    """Register both interfaces once; select one with
-    ``model.set_attn_implementation(ATTN_NAME)`` (:77-83)."""
+    """Registers both interfaces once; select one with
+    ``model.set_attn_implementation(ATTN_NAME)`` (qwen_paged_attn.py:77-83)."""
     from transformers import AttentionInterface
 
     for name, fn in ((ATTN_NAME, paged_bridge_attention),
@@ -127,67 +181,72 @@ def register():
             _registered.add(name)
 
 
-def _sync():
-    torch.cuda.synchronize()
+# --------------------------------------------------------------------------- drivers
 
-
-@torch.no_grad()
-def generate_greedy(model, input_ids, max_new_tokens, cache):
-    """Greedy decode through the bridge cache (:86-128).  Returns
-    ``(ids [1, n], ttft_s, tpot_s, step_logits)``; step_logits are the
-    next-token logits (prompt's last position, then every step) as CPU fp32."""
-    dev = input_ids.device
-    cache.reset()
-    set_active_cache(cache)
-    n0 = input_ids.shape[1]
-    _sync()
-    t0 = time.perf_counter()
-    logits = model(input_ids=input_ids, position_ids=torch.arange(n0, device=dev)[None],
-                   use_cache=False).logits[:, -1, :]
-    _sync()
-    ttft = time.perf_counter() - t0
-    step_logits = [logits[0].float().cpu()]
-    tok = logits.argmax(-1, keepdim=True)
-    out = [tok]
+def _run(model, cache, prompt_ids, n_tokens, pick, timed=False):
+    """Prompt, then the picked tokens: token i = pick(i, logits before it) is a
+    [1, 1] id tensor, fed as the next step unless it is the last.  Returns the
+    wall time of every model call (synchronized) when `timed`."""
     times = []
-    for i in range(max_new_tokens - 1):
-        pos = torch.tensor([[n0 + i]], device=dev)
-        _sync()
+
+    def call(session, ids):
+        if not timed:
+            return session.step(ids)
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
-        logits = model(input_ids=tok, position_ids=pos, use_cache=False).logits[:, -1, :]
-        _sync()
+        logits = session.step(ids)
+        torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
-        step_logits.append(logits[0].float().cpu())
+        return logits
+
+    with DecodeSession(model, cache) as s:
+        logits = call(s, prompt_ids)
+        for i in range(n_tokens):
+            tok = pick(i, logits)
+            if i + 1 < n_tokens:
+                logits = call(s, tok)
+    return times
+
+
+def generate_greedy(model, input_ids, max_new_tokens, cache):
+    """Greedy decode through the bridge (qwen_paged_attn.py:86-128).  Returns
+    ``(ids [1, n], ttft_s, tpot_s, step_logits)``: the time of the prompt call,
+    the mean time of the one-token calls, and the next-token logits before
+    every generated token (CPU fp32)."""
+    chosen, seen = [], []
+
+    def pick(i, logits):
+        seen.append(logits[0].float().cpu())
         tok = logits.argmax(-1, keepdim=True)
-        out.append(tok)
-    tpot = sum(times) / len(times) if times else float("nan")
-    return torch.cat(out, dim=1), ttft, tpot, step_logits
+        chosen.append(tok)
+        return tok
+
+    times = _run(model, cache, input_ids, max_new_tokens, pick, timed=True)
+    decode = times[1:]
+    tpot = sum(decode) / len(decode) if decode else float("nan")
+    return torch.cat(chosen, dim=1), times[0], tpot, seen
 
 
-@torch.no_grad()
 def teacher_force_logprobs(model, prompt_ids, cont_ids, cache):
-    """Log-probabilities the cache's variant gives the fixed continuation
-    ``cont_ids [1, n]`` after ``prompt_ids``, through the same prompt + decode
-    path as generate_greedy (:131-158).  Returns a list of n floats."""
-    dev = prompt_ids.device
-    cache.reset()
-    set_active_cache(cache)
-    n0 = prompt_ids.shape[1]
-    logits = model(input_ids=prompt_ids, position_ids=torch.arange(n0, device=dev)[None],
-                   use_cache=False).logits[:, -1, :]
-    logps = []
-    for i in range(cont_ids.shape[1]):
-        t = cont_ids[0, i]
-        logps.append(torch.log_softmax(logits[0].float(), dim=-1)[t].item())
-        logits = model(input_ids=t.view(1, 1), position_ids=torch.tensor([[n0 + i]], device=dev),
-                       use_cache=False).logits[:, -1, :]
-    return logps
+    """Natural-log probabilities the cache's variant gives the fixed
+    continuation ``cont_ids [1, n]`` after ``prompt_ids``, through the same
+    prompt + decode steps as generate_greedy (qwen_paged_attn.py:131-158).
+    Returns a list of n floats."""
+    cont = cont_ids[0]
+    picked = []
+
+    def pick(i, logits):
+        picked.append(torch.log_softmax(logits[0].float(), dim=-1)[cont[i]])
+        return cont[i].view(1, 1)
+
+    _run(model, cache, prompt_ids, cont.shape[0], pick)
+    return torch.stack(picked).cpu().tolist()
 
 
 def teacher_force_ppl(model, prompt_ids, cont_ids, cache):
-    """Perplexity of ``cont_ids`` under the cache's variant (:161-164)."""
+    """Perplexity of ``cont_ids`` under the cache's variant (qwen_paged_attn.py:161-164)."""
     lp = teacher_force_logprobs(model, prompt_ids, cont_ids, cache)
-    return float(torch.exp(torch.tensor(-sum(lp) / len(lp))))
+    return math.exp(-sum(lp) / len(lp))
 
 
 @torch.no_grad()

@@ -319,6 +319,36 @@ def test_paged_cache_class_host_logic():
                   torch.zeros(5, 2, 128, dtype=torch.float16))
 
 
+@pytest.mark.parametrize("int8", [False, True])
+def test_bench_gate_reference_matches_oracle(int8):
+    """bench.dense_reference (the correctness gate the benchmark runs before
+    timing each config) agrees with the oracle on the CPU, FP16 and INT8."""
+    import sys
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    from _cases import fp16_case, int8_case, oracle_fp16, oracle_int8
+
+    lens = np.array([300, 17, 1000], np.int32)
+    c = (int8_case if int8 else fp16_case)(3, lens, 12, 2, seed=5)
+    t = torch.from_numpy
+    if int8:
+        caches = [(t(c["k_cache8"]), t(c["v_cache8"]), t(c["k_scales"]), t(c["v_scales"]))]
+        bt, want = c["block_table8"], oracle_int8(c)
+    else:
+        caches = [(t(c["k_cache"]), t(c["v_cache"]), None, None)]
+        bt, want = c["block_table"], oracle_fp16(c)
+    case = dict(caches=caches, bt=t(bt), bs=16, lens=[int(x) for x in lens], head_dim=128,
+                q=t(c["q"]), scale=c["scale"])
+    for s in range(3):
+        got = bench.dense_reference(torch, case, s).numpy()
+        np.testing.assert_allclose(got, want[s], atol=1e-5, rtol=1e-5)
+    assert bench.gate_seqs([5, 9, 1, 7, 3, 2, 8]) == [0, 1, 2, 3, 4, 5, 6]
+    assert bench.gate_seqs([4] * 100, 2) == [0, 50, 99]
+
+
 def test_bench_dense_gather_inverts_the_paged_layout():
     """bench.gather_dense (the dense baseline's input) recovers the contiguous
     K/V that the oracle's builder scattered into the paged layout, repeated

@@ -150,6 +150,44 @@ def test_quant_write_near_ties(head_dim, pattern):
     run_case(T=96, hkv=2, d=head_dim, bs=16, pattern=pattern, seed=head_dim + 5, kv=kv)
 
 
+@pytest.mark.parametrize("pattern", ["prefill", "scattered"])
+def test_quant_write_matches_reference_golden_rows(pattern):
+    """Every fp16 row of the golden fixture (written by the reference's own
+    quantize_per_token, tests/golden/make_quant_golden.py), including the rows
+    with NaN and +-inf, goes through the write kernel: each token's int8
+    bytes must equal the reference's, and its scale too (bit for bit where
+    finite; NaN where the reference's is NaN)."""
+    import os
+
+    import pa_int8
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz"))
+    x = np.concatenate([z["x16"], z["xnf"]])                     # [R, 128]
+    q = np.concatenate([z["q16"], z["qnf"]])
+    sc = np.concatenate([z["s16"], z["snf"]])
+    R, d = x.shape
+    rng = np.random.default_rng(len(pattern))
+    T = R                                     # one token per row; K and V get the rows
+    k = x[:, None, :]                         # [T, 1, D]
+    v = x[::-1][:, None, :].copy()            # reversed order for V
+    bs, nb = 16, R + 4                        # room for one block per token
+    slots = slots_for(pattern, T, nb, bs, rng)
+    kc = torch.zeros((nb, 1, d // 8, bs, 8), dtype=torch.int8, device=DEV)
+    vc = torch.zeros((nb, 1, d, bs), dtype=torch.int8, device=DEV)
+    ks = torch.zeros((nb, 1, bs), dtype=torch.float32, device=DEV)
+    vs = torch.zeros_like(ks)
+    pa_int8.reshape_and_cache_int8(_t(k), _t(v), kc, vc, ks, vs, _t(slots))
+    torch.cuda.synchronize()
+    blk, off = slots // bs, slots % bs
+    gk = kc.cpu().numpy()[blk, 0, :, off, :].reshape(T, d)
+    gv = vc.cpu().numpy()[blk, 0, :, off]
+    assert np.array_equal(gk, q) and np.array_equal(gv, q[::-1])
+    for got, want in ((ks.cpu().numpy()[blk, 0, off], sc), (vs.cpu().numpy()[blk, 0, off], sc[::-1])):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
 def test_quant_write_single_token_append():
     """decode_append pattern (benchmarks/int8_bridge/paged_cache.py:132-156): T=batch."""
     run_case(T=5, hkv=4, d=128, bs=16, pattern="scattered", seed=3)

@@ -105,6 +105,27 @@ def test_bridge_entry_checks():
     br.set_active_cache(None)
 
 
+def test_sessions_are_scoped_to_their_context():
+    """A DecodeSession binds its cache only while it is entered, and restores
+    whatever was bound before it (nested sessions, set_active_cache)."""
+    from pa_int8 import qwen_bridge as br
+
+    class Cache:
+        is_int8 = False
+
+        def reset(self):
+            self.was_reset = True
+
+    outer, inner = Cache(), Cache()
+    br.set_active_cache(outer)
+    assert br._SESSION.get().cache is outer
+    with br.DecodeSession(None, inner) as s:
+        assert br._SESSION.get() is s and inner.was_reset and s.position == 0
+    assert br._SESSION.get().cache is outer
+    br.set_active_cache(None)
+    assert br._SESSION.get() is None
+
+
 def test_register_is_idempotent():
     from transformers import AttentionInterface
 

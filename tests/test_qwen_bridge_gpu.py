@@ -55,8 +55,8 @@ def test_fp16_bridge_matches_dense_reference(model, plen, n):
     err = np.abs(got - want)
     print(f"fp16 bridge, prompt {plen} + {n}: max |dlogp| {err.max():.2e}, mean {err.mean():.2e}")
     assert err.max() < LOGP_MAX
-    # every continuation token is fed (the last one's logits are unused): plen + n cached
-    assert cache.lengths == [plen + n] * model.config.num_hidden_layers
+    # every continuation token but the last (whose logits nobody reads) is fed
+    assert cache.lengths == [plen + n - 1] * model.config.num_hidden_layers
 
 
 def test_greedy_generation_follows_the_reference(model):
