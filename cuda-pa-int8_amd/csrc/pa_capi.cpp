@@ -26,10 +26,10 @@ hipError_t launch_decode(const DecodeLaunch& l) {
   }
 }
 
-int sched_groups(int head_dim, int waves, bool int8_kv) {
+int resident_groups(int head_dim, bool stream_part, int waves, bool int8_kv, int column_tiles) {
   switch (head_dim) {
 #define PA_CASE(D) \
-  case D: return sched_groups_d##D(waves, int8_kv);
+  case D: return resident_groups_d##D(stream_part, waves, int8_kv, column_tiles);
     PA_FOR_EACH_HEAD_DIM(PA_CASE)
 #undef PA_CASE
     default: return 0;
@@ -53,6 +53,7 @@ constexpr int kSchedMinPartition = 1024;   // per 4 waves, in-kernel schedule
 thread_local int g_waves_override = 0;
 thread_local int g_schedule_mode = 0;   // 0 auto, 1 grid, 2 in-kernel schedule
 thread_local int g_load_mode = 0;       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
+thread_local int g_head_tile_cap = 0;   // 0 auto, else the most query heads per work-group
 constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
 constexpr int kKntMinPartition = 4096;          // non-temporal K rows from this split size
 // Upper bound on resident decode work-groups used to size the partial
@@ -78,9 +79,10 @@ int ilog2(int v) {
   return r;
 }
 
-// Largest divisor of the GQA group size that fits one work-group's head tile.
-int head_tile_for(int group) {
-  for (int t = std::min(group, pa::kMaxGroupTile); t >= 1; --t)
+// Largest divisor of the GQA group size that fits one work-group's head tile
+// of at most `cap` query heads.
+int head_tile_for(int group, int cap) {
+  for (int t = std::min(group, cap); t >= 1; --t)
     if (group % t == 0) return t;
   return 1;
 }
@@ -95,6 +97,9 @@ struct Plan {
   // In-kernel schedule: partials hold rows_max slot rows of units_per_row
   // units; the kernel picks the partition in [pmin, pmax].
   bool sched = false;
+  // Stream partition: equal contiguous chunk ranges per work-group; the
+  // partials hold 2 slots per work-group.
+  bool stream = false;
   int rows_max = 0;
   int rows_min = 0;       // rows at the upper partition bound: the least the partials may hold
   int pmin = 0, pmax = 0;
@@ -108,7 +113,28 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
                int partition_tokens) {
   Plan p;
   const int group = num_heads / num_kv_heads;
-  p.head_tile = head_tile_for(group);
+  // Work distribution.  The split-K kinds (long and ragged contexts) use the
+  // in-kernel schedule: no empty work-groups and largest-first items (config
+  // 5 of the bench: 10-37% faster than the grid).  The single-launch kinds
+  // keep the grid, which saves the schedule's start-up for equal lengths.
+  const int mode = g_schedule_mode;
+  const long long cap = (long long)max_blocks * block_size;
+  p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
+  // The stream partition serves the split-K kinds (its merge is the reduce
+  // launch); its chunk list must count in 32 bits: at most S * ceil(cap / 32)
+  // chunks per kv head.
+  p.stream = mode == 3 && !is_fused(kind) &&
+             (long long)num_seqs * ((cap + 31) / 32) * num_heads < (1ll << 31);
+  if (num_seqs > pa::kSchedMaxSeqs) p.sched = p.stream = false;
+  if (p.stream) p.sched = false;
+  // Head tile: up to 32 query heads (two MFMA column tiles) for head_dim <=
+  // 128, except under the in-kernel schedule, which keeps 16.  (There, MQA
+  // 32/1 of bench config 5 ran no faster with one 32-head work-group per row
+  // than with two 16-head ones: the rows are too few to balance, 1.3 per
+  // resident work-group; INT8 49.4 -> 56.7 us.)
+  int tile_cap = (head_dim <= 128 && !p.sched) ? pa::kMaxHeadTile : pa::kMaxGroupTile;
+  if (g_head_tile_cap > 0) tile_cap = std::min(tile_cap, g_head_tile_cap);
+  p.head_tile = head_tile_for(group, tile_cap);
   p.nchunk = group / p.head_tile;
   p.units = num_seqs * num_kv_heads * p.nchunk;
   const int ov = g_waves_override;
@@ -120,8 +146,8 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // MQA 32/1 INT8 57.0 -> 48.7 us, MQA FP16 72.4 -> 67.1 us; uniform config 4
   // INT8 +0.5-1.3%; FP16 with one chunk gains nothing (ragged +1.4%).
   if (ov == 0 && !is_fused(kind) && (!is_f16(kind) || p.nchunk > 1)) p.waves = 4;
+  if (ov == 0 && p.stream) p.waves = 4;
   if (head_dim > 128) p.waves = 4;     // LDS of the 8-wave merge exceeds 64 KB
-  const long long cap = (long long)max_blocks * block_size;
   long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
   if (ctx < 1) ctx = 1;
   long long part;
@@ -157,18 +183,12 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   const int lm = g_load_mode;
   p.nt_loads = lm == 2 || (lm == 0 && p.nchunk == 1 && kv_bytes > kNtMinBytes);
 
-  // Work distribution.  The split-K kinds (long and ragged contexts) use the
-  // in-kernel schedule: no empty work-groups and largest-first items (config
-  // 5 of the bench: 10-37% faster than the grid).  The single-launch kinds
-  // keep the grid, which saves the schedule's start-up for equal lengths.
-  const int mode = g_schedule_mode;
-  p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
-  if (num_seqs > pa::kSchedMaxSeqs) p.sched = false;
   // K rows non-temporal as well: FP16 grid launches whose splits hold at least
   // kKntMinPartition tokens (same box, caches rotated over 4x the Infinity
   // Cache: config 3 FP16 89.6 -> 86.4 us; config 2's 1024-token splits and
   // INT8 measured faster with plain K).
-  p.k_nt = p.nt_loads && is_f16(kind) && !p.sched && p.partition >= kKntMinPartition;
+  p.k_nt = p.nt_loads && is_f16(kind) && !p.sched && !p.stream &&
+           p.partition >= kKntMinPartition;
   if (p.sched) {
     if (partition_tokens > 0) {
       p.pmin = p.pmax = p.pmin_uniform = p.partition;
@@ -206,6 +226,7 @@ struct WsLayout {
 };
 
 size_t slot_count(const Plan& p, int num_seqs) {
+  if (p.stream) return 2 * (size_t)kSchedGroupsBound;
   return p.sched ? (size_t)p.rows_max * p.units / std::max(1, num_seqs)
                  : (size_t)p.units * p.nsplit;
 }
@@ -213,7 +234,9 @@ size_t slot_count(const Plan& p, int num_seqs) {
 WsLayout ws_layout(const Plan& p, int head_dim, int num_seqs) {
   WsLayout w;
   const size_t slots = slot_count(p, num_seqs);
-  w.info = p.sched ? align_up((size_t)(1 + num_seqs) * sizeof(int)) : 0;
+  w.info = p.stream  ? align_up((size_t)(2 + num_seqs) * sizeof(int))
+           : p.sched ? align_up((size_t)(1 + num_seqs) * sizeof(int))
+                     : 0;
   w.ml = align_up(slots * p.head_tile * 2 * sizeof(float));
   w.acc = align_up(slots * p.head_tile * head_dim * sizeof(float));
   w.total = w.info + w.ml + w.acc;
@@ -244,6 +267,16 @@ pa_status_t decode_plan_call(const pa::DecodeCall& c, size_t ws_fit, Plan* plan,
     if (groups * p.waves * 64 > 0xFFFFFFFFll) return PA_ERR_BAD_SHAPE;
   }
   WsLayout wl = ws_layout(p, c.head_dim, c.num_seqs);
+  if (ws_fit > 0 && wl.total > ws_fit && p.stream) {
+    // the stream partition's partials do not fit: the in-kernel schedule,
+    // whose row capacity can shrink, serves the call
+    const int saved = g_schedule_mode;
+    g_schedule_mode = 2;
+    p = make_plan(c.kind, c.num_seqs, c.num_heads, c.num_kv_heads, c.head_dim, c.block_size,
+                  c.max_blocks, c.max_context_len, c.partition_tokens);
+    g_schedule_mode = saved;
+    wl = ws_layout(p, c.head_dim, c.num_seqs);
+  }
   if (ws_fit > 0 && wl.total > ws_fit) {
     if (!p.sched) return PA_ERR_SCRATCH_LIMIT;
     Plan lo = p;
@@ -297,13 +330,15 @@ pa_status_t decode_common(const pa::DecodeCall& c, void* counters, size_t counte
   l.part_ml = reinterpret_cast<float*>(ws + wl.info);
   l.part_acc = reinterpret_cast<float*>(ws + wl.info + wl.ml);
   l.sched = p.sched;
+  l.stream_part = p.stream;
   l.rows_max = p.rows_max;
   l.pmin = p.pmin;
   l.pmin_uniform = p.pmin_uniform;
   l.pmax = p.pmax;
-  if (p.sched) {
+  if (p.sched || p.stream) {
     const bool i8 = !is_f16(kind);
-    l.groups = pa::sched_groups(head_dim, p.waves, i8);
+    l.groups = pa::resident_groups(head_dim, p.stream, p.waves, i8,
+                                   p.head_tile > pa::kMaxGroupTile ? 2 : 1);
     if (l.groups <= 0) return PA_ERR_LAUNCH;
     l.groups = std::min(l.groups, kSchedGroupsBound);
   }
@@ -441,13 +476,22 @@ pa_status_t pa_decode_set_waves_per_group(int32_t waves) {
 size_t pa_decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
   if (num_heads < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0) return 0;
   const int group = num_heads / num_kv_heads;
-  const int units = std::max(0, num_seqs) * num_kv_heads * (group / head_tile_for(group));
+  // Head tiles of at most 16 query heads (the head_dim-256 rule): the most
+  // units any head_dim gives, so the bound holds without knowing it.
+  const int units =
+      std::max(0, num_seqs) * num_kv_heads * (group / head_tile_for(group, pa::kMaxGroupTile));
   return counter_region(units);
 }
 
 pa_status_t pa_decode_set_schedule(int32_t mode) {
-  if (mode < 0 || mode > 2) return PA_ERR_BAD_SHAPE;
+  if (mode < 0 || mode > 3) return PA_ERR_BAD_SHAPE;
   g_schedule_mode = mode;
+  return PA_OK;
+}
+
+pa_status_t pa_decode_set_max_head_tile(int32_t heads) {
+  if (heads != 0 && heads != 16 && heads != 32) return PA_ERR_BAD_SHAPE;
+  g_head_tile_cap = heads;
   return PA_OK;
 }
 

@@ -13,7 +13,8 @@ namespace pa {
 hipError_t PA_CAT(launch_decode_d, PA_HEAD_DIM)(const DecodeLaunch& l) {
   return launch_decode_d<PA_HEAD_DIM>(l);
 }
-int PA_CAT(sched_groups_d, PA_HEAD_DIM)(int waves, bool int8_kv) {
-  return sched_groups_d<PA_HEAD_DIM>(waves, int8_kv);
+int PA_CAT(resident_groups_d, PA_HEAD_DIM)(bool stream_part, int waves, bool int8_kv,
+                                            int column_tiles) {
+  return resident_groups_d<PA_HEAD_DIM>(stream_part, waves, int8_kv, column_tiles);
 }
 }  // namespace pa

@@ -149,17 +149,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 constexpr int kPolicyDevice = 16;
 
 // Merge the `ns` partials of one unit (gt heads) and write its fp16 output
-// rows.  The partial of split sp sits in slot slot0 + sp * stride: acc[gt][D]
+// rows.  The partial of split sp sits in slot slot_of(sp): acc[gt][D]
 // (relative to its max) and (m, l) per head.  Thread i owns (head, 4-dim
 // chunk) items i, i + THREADS, ... and merges them without LDS or barriers:
 // the (m, l) pairs and accumulators of 8 splits at a time are loaded in one
 // batch and folded into a running (max, sum, acc).
 // COHERENT: device-coherent loads (partials written in this launch).
-template <int D, int THREADS, bool COHERENT>
+template <int D, int THREADS, bool COHERENT, typename SlotOf>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
                                              const float* __restrict__ pml,
-                                             half_t* __restrict__ out, size_t slot0, int stride,
-                                             int gt, size_t out_base, int ns) {
+                                             half_t* __restrict__ out, SlotOf slot_of, int gt,
+                                             size_t out_base, int ns) {
   constexpr int CH = D / 4;
   constexpr int SB = 8;
   constexpr int POL = COHERENT ? kPolicyDevice : 0;
@@ -178,7 +178,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
       for (int u = 0; u < SB; ++u) {
         // Past the last split the last one is re-read (and weighted 0), so
         // every load of the batch is unconditional.
-        const size_t slot = slot0 + (size_t)min(s0 + u, ns - 1) * stride;
+        const size_t slot = slot_of(min(s0 + u, ns - 1));
         const auto ra = buf_rsrc(pacc + slot * gt * D, acc_bytes);
         const auto rm = buf_rsrc(pml + slot * gt * 2, ml_bytes);
         v[u] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * c) * 4, 0, POL));
@@ -221,7 +221,7 @@ constexpr int kWavesPerCU = 8;
 constexpr size_t kLdsPerCU = 160 * 1024 - 4096;   // (margin for allocation granularity)
 
 template <int D, int NW>
-struct alignas(16) DecodeSmem {
+struct alignas(16) DecodeSmem {   // (one column tile at a time)
   float a[NW][16][D + kMergeRowPad];   // each wave's accumulator: per head, per dim (+ pad)
   float m[NW][16];
   float l[NW][16];
@@ -239,16 +239,575 @@ struct SplitWork {
   int stride;      // partial slots between consecutive splits
 };
 
-// The decode of one split.  FUSED: partials are written device-coherent and
-// the last work-group of the unit merges them (single launch).  DIRECT1: a
-// unit with one split writes its output here (else the split-K reduce does).
+// Where one decode call's caches live (the same for every wave).
+struct CacheView {
+  const uint8_t* kc;
+  const uint8_t* vc;
+  const float* ksc;   // INT8 only
+  const float* vsc;
+  int hkv;            // kv heads
+  int bs;             // block size (a power of two)
+  int num_blocks;     // valid block ids are [0, num_blocks)
+};
+
+// The work of one wave on one 32- or 64-token chunk of one (sequence, kv
+// head) stream at a time: its K/V/scale loads, the QK product, the online
+// softmax and the PV product, and the running state of its query heads.  CT:
+// 16-head MFMA column tiles (1, or 2 for head tiles of 17..32 query heads:
+// each K/V register load then feeds both tiles).  The decode kernels drive it
+// with block ids from wherever they keep them (LDS for a split, registers
+// for a stream); all positions are tokens of the stream.
+//
+// Token layout of a chunk starting at tok0, for lane (r = lane & 15, g = lane >> 4):
+//   K rows: token tok0 + 32p + 8(r>>2) + (r&3) feeds MFMA row r of pair p's first QK
+//           MFMA, + 4 its second (W8: tokens tok0 + 16(r>>2) + 8p + 2(r&3) and + 1);
+//   scores / V: the lane's 8 score tokens are tok0 + 32p + 8g .. +7 (W8: tok0 + 16g +
+//           8p .. +7), exactly its P^T operand of PV, and its V rows are dims 16t + r.
+// A token at or past t_end is read at token `fb` instead (a valid token of the
+// same stream: its block id is looked up the same way) and masked.
+template <int D, int CT, bool I8>
+struct DecodeWave {
+  static_assert(D % 16 == 0 && D >= 64 && D <= 256, "head_dim: a multiple of 16 in [64, 256]");
+  static_assert(CT == 1 || (CT == 2 && D <= 128), "two column tiles only for head_dim <= 128");
+  static constexpr int KC = (D + 31) / 32;   // 32-dim k-chunks of one QK product
+  static constexpr int NT = D / 16;          // 16-dim output tiles of PV
+  static constexpr int DG = D / 8;           // 8-dim groups of a K row
+  // With head_dim % 32 == 16 the last k-chunk holds 16 dims: its dim groups
+  // 4(KC-1) + g for g >= 2 lie past the row.  Those lanes load the row's last
+  // group instead (in bounds) and feed zeros to the MFMA; their query
+  // operand is zero as well.
+  static constexpr bool KPAD = (D % 32) != 0;
+  // 32-token pairs per chunk: two, except with head_dim 256 (whose
+  // accumulators are twice as large) and with two column tiles (whose query
+  // operands, scores and accumulators are twice as many); either way the
+  // registers of one wave stay within the 256 of two waves per SIMD.
+  static constexpr int PAIRS = (D <= 128 && CT == 1) ? 2 : 1;
+  static constexpr int IT = 32 * PAIRS;      // tokens per chunk
+  static constexpr int ESZ = I8 ? 1 : 2;     // bytes per cache element
+  using LVec = typename std::conditional<I8, uint2, uint4>::type;   // 8 elements
+  // INT8 with head_dim <= 128 and one column tile uses 16-byte loads
+  // throughout (W8): a K load holds one dim group of two adjacent tokens (t,
+  // t + 1), which feed the same row of the two QK MFMAs of a pair, and a V
+  // load holds 16 tokens of one dim, which feed both pairs.  Each lane loads
+  // the scales of 4 tokens and the others reach the lanes that need them by
+  // quad DPP broadcasts.
+  static constexpr bool W8 = I8 && D <= 128 && CT == 1;
+
+  // Block ids of a lane's K rows and V rows (W8: one 16-token group each).
+  struct Blocks {
+    int kb[PAIRS];
+    int vb[PAIRS];
+  };
+  // W8: the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i and the valid
+  // tokens among the lane's 8 of each pair.  They are loaded one chunk
+  // ahead, with the K rows, so the softmax does not wait for the V rows (the
+  // memory counter completes in order): `wa` holds the next chunk's, and
+  // each chunk copies them out before loading the following ones.
+  struct W8Buf {
+    float4 ks4, vs4;
+    int nvalid[PAIRS];
+  };
+
+  int r, g;
+  // Running (max, sum) of query head r + 16 ct, its accumulator (dims 16t +
+  // 4g + e), and the exponent the INT8 weights are scaled by (FP16: 14).
+  float m_run[CT], l_part[CT];
+  f4_t acc[CT][NT];
+  int e_cur;
+  // Query operand: lane (r, g) holds q[head r + 16 ct][32kk + 8g .. +7]; INT8:
+  // the K bias 1152 * sum(q) per head.
+  h8_t qreg[CT][KC];
+  float qbias[CT];
+  // Loads of the chunk in flight.
+  LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
+  float ksv[PAIRS][8], vsv[PAIRS][8];   // INT8 scales of this lane's 8 tokens
+  int nvalid[PAIRS];                    // valid tokens among this lane's 8
+  uint4 kw[PAIRS][KC];                  // W8: K rows of tokens (t, t + 1)
+  uint4 vw[NT];                         // W8: V rows of 16 tokens
+  W8Buf wa;
+
+  __device__ __forceinline__ void init(int lane) {
+    r = lane & 15;
+    g = lane >> 4;
+    reset();
+  }
+
+  // Empty state: no token seen yet.
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      m_run[ct] = kNegInf;
+      l_part[ct] = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[ct][t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    e_cur = I8 ? 0 : 14;
+  }
+
+  // The query operand of the gt heads starting at q row `row0` (sequence *
+  // num_heads + first head).
+  __device__ __forceinline__ void load_q(const half_t* __restrict__ q, size_t row0, int gt) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const bool hv = r + 16 * ct < gt;
+      const half_t* qrow = q + (row0 + (hv ? r + 16 * ct : 0)) * D + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        const bool dv = !KPAD || kk < KC - 1 || 4 * kk + g < DG;
+        const uint4 v = (hv && dv) ? *reinterpret_cast<const uint4*>(qrow + 32 * kk)
+                                   : make_uint4(0, 0, 0, 0);
+        qreg[ct][kk] = __builtin_bit_cast(h8_t, v);
+      }
+    }
+  }
+
+  // INT8: the K bias of each head, once the query operand has arrived.
+  __device__ __forceinline__ void compute_qbias() {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      qbias[ct] = 0.f;
+      if constexpr (I8) {
+        float s = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+          const uint4 v = __builtin_bit_cast(uint4, qreg[ct][kk]);
+          s = dot2(v.x, 0x3C003C00u, s);
+          s = dot2(v.y, 0x3C003C00u, s);
+          s = dot2(v.z, 0x3C003C00u, s);
+          s = dot2(v.w, 0x3C003C00u, s);
+        }
+        qbias[ct] = 1152.f * head_sum(s);
+      }
+    }
+  }
+
+  // The tokens whose block ids this lane's loads of the chunk at tok0 need
+  // (out-of-range tokens replaced by fb): kt for the K rows, vt for the V rows.
+  __device__ __forceinline__ void block_tokens(int tok0, int t_end, int fb, int (&kt)[PAIRS],
+                                               int (&vt)[PAIRS]) const {
+    if constexpr (W8) {
+      // K rows of lane (r, g) lie in the 16-token group tok0 + 16(r >> 2), its V
+      // rows and scales in tok0 + 16g; a group never straddles a block
+      // (block_size is a multiple of 16).
+      const int kg = tok0 + 16 * (r >> 2);
+      const int tg = tok0 + 16 * g;
+      kt[0] = kg < t_end ? kg : fb;
+      vt[0] = tg < t_end ? tg : fb;
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int kg = tok0 + 32 * p + 8 * (r >> 2);
+      const int tg = tok0 + 32 * p + 8 * g;
+      kt[p] = kg < t_end ? kg : fb;
+      vt[p] = tg < t_end ? tg : fb;
+    }
+  }
+
+  // Dim-group offset (relative to the lane's group g) of k-chunk kk's K row
+  // load: 4 kk, or for the padding lanes of a 16-dim last chunk the row's
+  // last group.
+  __device__ __forceinline__ int kgroup(int kk) const {
+    return (!KPAD || 4 * kk + g < DG) ? 4 * kk : DG - 1 - g;
+  }
+
+  // K rows of kv head kvh.
+  template <bool KNT>
+  __device__ __forceinline__ void issue_k(const CacheView& cv, int kvh, int tok0, int t_end, int fb,
+                                          const Blocks& b) {
+    if constexpr (W8) {
+      // Row r of pair p: tokens tok0 + 16(r >> 2) + 8p + 2(r & 3) and + 1.
+      const int kg = tok0 + 16 * (r >> 2);
+      const int kgc = kg < t_end ? kg : fb;
+      const int kb = (unsigned)b.kb[0] < (unsigned)cv.num_blocks ? b.kb[0] : 0;
+      const uint8_t* kp = cv.kc + ((((size_t)kb * cv.hkv + kvh) * (D / 8) + g) * cv.bs +
+                                   (kgc & (cv.bs - 1)) + 2 * (r & 3)) * 8;
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk)
+          kw[p][kk] = load_tile<uint4, KNT>(kp + (size_t)kgroup(kk) * cv.bs * 8 + 64 * p);
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int kg = tok0 + 32 * p + 8 * (r >> 2);
+      const int kgc = kg < t_end ? kg : fb;
+      const int kb = (unsigned)b.kb[p] < (unsigned)cv.num_blocks ? b.kb[p] : 0;
+      const int koff = (kgc & (cv.bs - 1)) + (r & 3);
+      const uint8_t* kp =
+          cv.kc + ((((size_t)kb * cv.hkv + kvh) * (D / 8) + g) * cv.bs + koff) * 8 * ESZ;
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        const uint8_t* p0 = kp + (size_t)kgroup(kk) * cv.bs * 8 * ESZ;
+        kx[p][kk] = load_tile<LVec, KNT>(p0);
+        ky[p][kk] = load_tile<LVec, KNT>(p0 + 4 * 8 * ESZ);
+      }
+    }
+  }
+
+  // W8: the scales and valid counts of a chunk (see W8Buf).
+  __device__ __forceinline__ void issue_scales(const CacheView& cv, int kvh, int tok0, int t_end,
+                                               int fb, const Blocks& b, W8Buf& B) const {
+    const int tg = tok0 + 16 * g;
+    const int tgc = tg < t_end ? tg : fb;
+    const bool vok = (unsigned)b.vb[0] < (unsigned)cv.num_blocks;
+    const int vb = vok ? b.vb[0] : 0;
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int t0 = tg + 8 * p;
+      B.nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
+    }
+    const size_t slot = ((size_t)vb * cv.hkv + kvh) * cv.bs + (tgc & (cv.bs - 1)) + 4 * (r & 3);
+    // (plain loads: a scale line holds several kv heads' scales)
+    B.ks4 = *reinterpret_cast<const float4*>(cv.ksc + slot);
+    B.vs4 = *reinterpret_cast<const float4*>(cv.vsc + slot);
+  }
+
+  // Where a chunk's V rows (and INT8 scales) are, once its block ids are
+  // known: lets a caller reuse the block-id registers before issuing them.
+  struct VPlan {
+    const uint8_t* vp[PAIRS];   // the lane's first V row of each pair
+    size_t slot[PAIRS];         // its tokens' first scale (INT8, not W8)
+    int nvalid[PAIRS];          // valid tokens among its 8 of each pair (not W8)
+  };
+
+  __device__ __forceinline__ VPlan plan_v(const CacheView& cv, int kvh, int tok0, int t_end,
+                                          int fb, const Blocks& b) const {
+    VPlan v;
+    if constexpr (W8) {
+      // V rows: dim 16t + r, tokens tok0 + 16g .. + 15 (pair p uses 8p .. 8p + 7).
+      const int tg = tok0 + 16 * g;
+      const int tgc = tg < t_end ? tg : fb;
+      const int vb = (unsigned)b.vb[0] < (unsigned)cv.num_blocks ? b.vb[0] : 0;
+      v.vp[0] = cv.vc + (((size_t)vb * cv.hkv + kvh) * D + r) * cv.bs + (tgc & (cv.bs - 1));
+      return v;
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int tg = tok0 + 32 * p + 8 * g;
+      const bool tin = tg < t_end;
+      const int tgc = tin ? tg : fb;
+      const bool vok = (unsigned)b.vb[p] < (unsigned)cv.num_blocks;
+      const int vb = vok ? b.vb[p] : 0;
+      const int voff = tgc & (cv.bs - 1);
+      v.nvalid[p] = (tin && vok) ? min(8, t_end - tg) : 0;
+      v.slot[p] = ((size_t)vb * cv.hkv + kvh) * cv.bs + voff;
+      v.vp[p] = cv.vc + ((((size_t)vb * cv.hkv + kvh) * D + r) * cv.bs + voff) * ESZ;
+    }
+    return v;
+  }
+
+  // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7,
+  // with their INT8 scales (not W8, which loads them with the K rows).
+  template <bool NTL>
+  __device__ __forceinline__ void issue_v(const CacheView& cv, const VPlan& v) {
+    if constexpr (W8) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) vw[t] = load_tile<uint4, NTL>(v.vp[0] + (size_t)(16 * t) * cv.bs);
+      return;
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      nvalid[p] = v.nvalid[p];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        vr[p][t] = load_tile<LVec, NTL>(v.vp[p] + (size_t)(16 * t) * cv.bs * ESZ);
+      if constexpr (I8) {
+        const float4 a0 = *reinterpret_cast<const float4*>(cv.ksc + v.slot[p]);
+        const float4 a1 = *reinterpret_cast<const float4*>(cv.ksc + v.slot[p] + 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(cv.vsc + v.slot[p]);
+        const float4 b1 = *reinterpret_cast<const float4*>(cv.vsc + v.slot[p] + 4);
+        ksv[p][0] = a0.x; ksv[p][1] = a0.y; ksv[p][2] = a0.z; ksv[p][3] = a0.w;
+        ksv[p][4] = a1.x; ksv[p][5] = a1.y; ksv[p][6] = a1.z; ksv[p][7] = a1.w;
+        vsv[p][0] = b0.x; vsv[p][1] = b0.y; vsv[p][2] = b0.z; vsv[p][3] = b0.w;
+        vsv[p][4] = b1.x; vsv[p][5] = b1.y; vsv[p][6] = b1.z; vsv[p][7] = b1.w;
+      }
+    }
+  }
+
+  template <bool NTL>
+  __device__ __forceinline__ void issue_v(const CacheView& cv, int kvh, int tok0, int t_end,
+                                          int fb, const Blocks& b) {
+    issue_v<NTL>(cv, plan_v(cv, kvh, tok0, t_end, fb, b));
+  }
+
+  // Tokens past the end or in invalid blocks exist only in the last chunk of
+  // a stream or split (or with a corrupt block table).
+  __device__ __forceinline__ bool mask_needed(const W8Buf& B) const {
+    bool short_lane = false;
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      if constexpr (W8) short_lane = short_lane || B.nvalid[p] < 8;
+      else short_lane = short_lane || nvalid[p] < 8;
+    }
+    return __builtin_amdgcn_ballot_w64(short_lane) != 0;
+  }
+
+  // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r + 16 ct
+  // (W8: tok0 + 16g + 8p + j); each converted K operand feeds every tile.
+  __device__ __forceinline__ void qk(float (&s)[CT][PAIRS][8]) const {
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      f4_t sx[CT], sy[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        sx[ct] = (f4_t){0.f, 0.f, 0.f, 0.f};
+        sy[ct] = (f4_t){0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        h8_t ax, ay;
+        if constexpr (W8) {
+          ax = i8x8_biased(make_uint2(kw[p][kk].x, kw[p][kk].y));   // token T
+          ay = i8x8_biased(make_uint2(kw[p][kk].z, kw[p][kk].w));   // token T + 1
+        } else if constexpr (I8) {
+          ax = i8x8_biased(kx[p][kk]);
+          ay = i8x8_biased(ky[p][kk]);
+        } else {
+          ax = __builtin_bit_cast(h8_t, kx[p][kk]);
+          ay = __builtin_bit_cast(h8_t, ky[p][kk]);
+        }
+        if (KPAD && kk == KC - 1 && 4 * kk + g >= DG) {
+          ax = (h8_t){};   // padding lanes of the last k-chunk (their q is zero too)
+          ay = (h8_t){};
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          sx[ct] = mfma16(ax, qreg[ct][kk], sx[ct]);
+          sy[ct] = mfma16(ay, qreg[ct][kk], sy[ct]);
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (W8) {
+            // rows 4g + e: tokens tok0 + 16g + 8p + 2e (sx) and + 1 (sy)
+            s[ct][p][2 * e] = sx[ct][e];
+            s[ct][p][2 * e + 1] = sy[ct][e];
+          } else {
+            s[ct][p][e] = sx[ct][e];
+            s[ct][p][4 + e] = sy[ct][e];
+          }
+        }
+    }
+  }
+
+  // ---- online softmax (lane-local except the per-head max) and PV.  c:
+  // the softmax scale times log2(e); B: the chunk's W8 scales.
+  __device__ __forceinline__ void softmax_pv(float (&s)[CT][PAIRS][8], bool need_mask, W8Buf& B,
+                                             float c) {
+    // W8: this lane's 4 scales; token 16g + 8p + j of the lane's row is held
+    // by quad position 2p + (j >> 2), element j & 3.
+    float ksa[4] = {B.ks4.x, B.ks4.y, B.ks4.z, B.ks4.w};
+    float vsa[4] = {B.vs4.x, B.vs4.y, B.vs4.z, B.vs4.w};
+    auto nval = [&](int p) {
+      if constexpr (W8) return B.nvalid[p];
+      else return nvalid[p];
+    };
+    if constexpr (W8) {
+      if (need_mask) {
+        // the row's valid tokens are its first nvalid[0] + nvalid[1]
+        const int n16 = B.nvalid[0] + B.nvalid[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vsa[i] = 4 * (r & 3) + i < n16 ? vsa[i] : 0.f;
+      }
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float ksj = quad_bcast(ksa[j & 3], 2 * p + (j >> 2));
+          s[0][p][j] = (s[0][p][j] - qbias[0]) * (ksj * c);
+        }
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            float v;
+            if constexpr (I8) v = (s[ct][p][j] - qbias[ct]) * (ksv[p][j] * c);
+            else v = s[ct][p][j] * c;
+            s[ct][p][j] = v;
+          }
+    }
+    if (need_mask) {
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) s[ct][p][j] = j < nval(p) ? s[ct][p][j] : kNegInf;
+          if constexpr (I8 && !W8) vsv[p][j] = j < nval(p) ? vsv[p][j] : 0.f;
+        }
+    }
+    float m_use[CT], alpha_m[CT], alpha_acc[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float mloc = kNegInf;
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mloc = fmaxf(mloc, s[ct][p][j]);
+      const float m_new = fmaxf(m_run[ct], head_max(mloc));
+      m_use[ct] = m_new == kNegInf ? 0.f : m_new;
+      alpha_m[ct] = exp2f_fast(m_run[ct] - m_use[ct]);   // rescales l
+      alpha_acc[ct] = alpha_m[ct];                       // rescales acc (incl. weight exponent)
+      m_run[ct] = m_new;
+    }
+    float wsc;
+    if constexpr (I8) {
+      float msv = 0.f;
+      if constexpr (W8) {
+        // The 64 tokens' scales are spread over the quads of a row and the 4 rows.
+        msv = fmaxf(fmaxf(vsa[0], vsa[1]), fmaxf(vsa[2], vsa[3]));
+        msv = fmaxf(msv, dpp_mov<kQuadXor1>(msv));
+        msv = fmaxf(msv, dpp_mov<kQuadXor2>(msv));
+      } else {
+#pragma unroll
+        for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
+      }
+      // Every head's lanes see the same tokens, so this max is wave-uniform.
+      msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
+      // Keep the weight exponent while the largest weight stays in [2^12, 2^15);
+      // it is shared by every head (the scales belong to the tokens).
+      const float top = __builtin_amdgcn_ldexpf(msv, e_cur);
+      if (msv > 0.f && (top >= 32768.f || top < 4096.f)) {
+        int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
+        e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          alpha_acc[ct] = __builtin_amdgcn_ldexpf(alpha_m[ct], e_new - e_cur);
+        e_cur = e_new;
+      }
+      wsc = __builtin_amdgcn_ldexpf(1.f, e_cur);
+    } else {
+      wsc = 16384.f;
+    }
+    h8_t pb[CT][PAIRS];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float lsum = 0.f;
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float pj = exp2f_fast(s[ct][p][j] - m_use[ct]);
+          lsum += pj;
+          float wj;
+          if constexpr (W8) wj = pj * quad_bcast(vsa[j & 3], 2 * p + (j >> 2)) * wsc;
+          else if constexpr (I8) wj = pj * vsv[p][j] * wsc;
+          else wj = pj * wsc;
+          pb[ct][p][j] = (half_t)wj;
+        }
+      }
+      l_part[ct] = l_part[ct] * alpha_m[ct] + lsum;
+      if (__builtin_amdgcn_ballot_w64(alpha_acc[ct] != 1.f) != 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[ct][t] *= alpha_acc[ct];
+      }
+    }
+
+    // ---- PV: each converted V operand feeds every column tile
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        h8_t av;
+        if constexpr (W8) {
+          av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y) : make_uint2(vw[t].z, vw[t].w));
+        } else if constexpr (I8) {
+          av = i8x8_exact(vr[p][t]);
+        } else {
+          uint4 v = vr[p][t];
+          if (need_mask) v = keep_first(v, nval(p));
+          av = __builtin_bit_cast(h8_t, v);
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct][t] = mfma16(av, pb[ct][p], acc[ct][t]);
+      }
+    }
+  }
+
+  // The wave's state of column tile ct into the merge slots of LDS: (max,
+  // sum) and the accumulator of head r (the tile's heads below nh).
+  template <typename Smem>
+  __device__ __forceinline__ void store_state(Smem& sm, int w, int ct, int nh) const {
+    if (r >= nh) return;
+    const float l_run = head_sum(l_part[ct]);
+    const float unscale = __builtin_amdgcn_ldexpf(1.f, -e_cur);
+    if (g == 0) {
+      sm.m[w][r] = m_run[ct];
+      sm.l[w][r] = l_run;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<f4_t*>(&sm.a[w][r][16 * t + 4 * g]) = acc[ct][t] * unscale;
+  }
+};
+
+// The NW wave states of column tile ct in LDS, merged per (head, 4-dim
+// chunk) item by the work-group's threads: the normalised fp16 output when
+// `final_out`, else a partial (acc, then (max, sum) per head) through the
+// buffer resources racc / rml (device-coherent stores when COHERENT).
+template <int D, int NW, bool COHERENT, typename Smem>
+__device__ __forceinline__ void merge_wave_states(const Smem& sm, int ct, int nh,
+                                                  int tid, bool final_out,
+                                                  half_t* __restrict__ out, size_t out_base,
+                                                  __amdgpu_buffer_rsrc_t racc,
+                                                  __amdgpu_buffer_rsrc_t rml) {
+  constexpr int CH = D / 4;
+  for (int i = tid; i < nh * CH; i += NW * kWave) {
+    const int hh = i / CH, c = i - hh * CH;
+    const int h = 16 * ct + hh;             // head within the unit's tile
+    float mw[NW], M = kNegInf;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      mw[v] = sm.m[v][hh];
+      M = fmaxf(M, mw[v]);
+    }
+    f4_t A = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float f = mw[v] == kNegInf ? 0.f : exp2f_fast(mw[v] - M);
+      L += sm.l[v][hh] * f;
+      A += *reinterpret_cast<const f4_t*>(&sm.a[v][hh][4 * c]) * f;
+    }
+    if (final_out) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      const uint2 pk =
+          make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
+      *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
+    } else {
+      // COHERENT: device-coherent (write-through) stores, visible to every XCD
+      // once this thread's stores are acknowledged.
+      constexpr int POL = COHERENT ? kPolicyDevice : 0;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc,
+                                             (h * D + 4 * c) * 4, 0, POL);
+      if (c == 0) {
+        const f2_t ml = {M, L};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml), rml, h * 8, 0, POL);
+      }
+    }
+  }
+}
+
+// The decode of one split of one unit by a whole work-group.  FUSED:
+// partials are written device-coherent and the last work-group of the unit
+// merges them (single launch).  DIRECT1: a unit with one split writes its
+// output here (else the split-K reduce does).
 // `after_issue` runs in every wave once the wave's first K/V loads are issued
 // (the scheduled kernel claims its next item there, so that no wait for this
 // split's data also waits for the claim).
 // `resolve(ctx, ns)` supplies the context length and split count once the
 // split's block-id loads are in flight (the grid kernel reads them from
 // memory then) and returns false when the split holds no tokens.
-template <int D, int NW, bool I8, bool FUSED, bool DIRECT1, bool NTL, bool KNT,
+template <int D, int NW, int CT, bool I8, bool FUSED, bool DIRECT1, bool NTL, bool KNT,
           typename Resolve, typename AfterIssue>
 __device__ __forceinline__ void decode_split(
     const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
@@ -256,25 +815,12 @@ __device__ __forceinline__ void decode_split(
     half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
     uint32_t* __restrict__ cnt, const DecodeShape& sh, SplitWork wk,
     DecodeSmem<D, NW>& sm, Resolve&& resolve, AfterIssue&& after_issue) {
-  static_assert(D % 16 == 0 && D >= 64 && D <= 256, "head_dim: a multiple of 16 in [64, 256]");
-  constexpr int KC = (D + 31) / 32;          // 32-dim k-chunks of one QK product
-  constexpr int NT = D / 16;                 // 16-dim output tiles of PV
-  constexpr int DG = D / 8;                  // 8-dim groups of a K row
-  // With head_dim % 32 == 16 the last k-chunk holds 16 dims: its dim groups
-  // 4(KC-1) + g for g >= 2 lie past the row.  Those lanes load the row's last
-  // group instead (in bounds) and feed zeros to the MFMA; their query
-  // operand is zero as well.
-  constexpr bool KPAD = (D % 32) != 0;
-  constexpr int PAIRS = D <= 128 ? 2 : 1;    // 32-token pairs per wave iteration
-  constexpr int IT = 32 * PAIRS;             // tokens per wave iteration
-  constexpr int ESZ = I8 ? 1 : 2;            // bytes per cache element
-  using LVec = typename std::conditional<I8, uint2, uint4>::type;   // 8 elements
-  // INT8 with head_dim <= 128 uses 16-byte loads throughout (W8): a K load
-  // holds one dim group of two adjacent tokens (t, t + 1), which feed the
-  // same row of the two QK MFMAs of a pair, and a V load holds 16 tokens of
-  // one dim, which feed both pairs.  Each lane loads the scales of 4 tokens
-  // and the others reach the lanes that need them by quad DPP broadcasts.
-  constexpr bool W8 = I8 && D <= 128;
+  using Wave = DecodeWave<D, CT, I8>;
+  using Blocks = typename Wave::Blocks;
+  using W8Buf = typename Wave::W8Buf;
+  constexpr int PAIRS = Wave::PAIRS;
+  constexpr int IT = Wave::IT;
+  constexpr bool W8 = Wave::W8;
 
   const int seq = wk.seq, kvh = wk.kvh, chunk = wk.chunk, split = wk.split;
   const int gt = sh.head_tile;
@@ -287,19 +833,15 @@ __device__ __forceinline__ void decode_split(
   asm volatile("" : "+v"(tid));
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
   const int head0 = kvh * sh.group + chunk * gt;
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
   const int* btrow = bt + (size_t)seq * sh.max_blocks;
-  const int bs = sh.block_size, bsl = sh.bs_log2;
-  const int hkv = sh.num_kv_heads;
-
-  float m_run = kNegInf, l_part = 0.f;
-  f4_t acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
-  int e_cur = I8 ? 0 : 14;
+  const int bsl = sh.bs_log2;
+  const CacheView cv{kc, vc, ksc, vsc, sh.num_kv_heads, sh.block_size, sh.num_blocks};
   const float c = sh.scale_log2;
+
+  Wave dw;
+  dw.init(lane);
 
   // ---- the split's block ids, staged once in LDS.  Their loads cover every
   // block the split can touch and are issued before the context length is
@@ -314,32 +856,8 @@ __device__ __forceinline__ void decode_split(
     const int i = tid + k * NW * kWave;
     staged[k] = i < nstage ? btrow[b_first + i] : 0;
   }
-  // ---- query operand: lane (r, g) holds q[head r][32kk + 8g .. +7]
-  h8_t qreg[KC];
-  {
-    const bool hv = r < gt;
-    const half_t* qrow = q + ((size_t)seq * sh.num_heads + head0 + (hv ? r : 0)) * D + 8 * g;
-#pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
-      const bool dv = !KPAD || kk < KC - 1 || 4 * kk + g < DG;
-      const uint4 v = (hv && dv) ? *reinterpret_cast<const uint4*>(qrow + 32 * kk)
-                                 : make_uint4(0, 0, 0, 0);
-      qreg[kk] = __builtin_bit_cast(h8_t, v);
-    }
-  }
-  float qbias = 0.f;
-  if constexpr (I8) {
-    float s = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
-      const uint4 v = __builtin_bit_cast(uint4, qreg[kk]);
-      s = dot2(v.x, 0x3C003C00u, s);
-      s = dot2(v.y, 0x3C003C00u, s);
-      s = dot2(v.z, 0x3C003C00u, s);
-      s = dot2(v.w, 0x3C003C00u, s);
-    }
-    qbias = 1152.f * head_sum(s);
-  }
+  dw.load_q(q, (size_t)seq * sh.num_heads + head0, gt);
+  dw.compute_qbias();
 
   if (!resolve(wk.ctx, wk.ns)) return;   // work-group uniform, before any barrier
   const int ns_eff = wk.ns;
@@ -356,421 +874,83 @@ __device__ __forceinline__ void decode_split(
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   __builtin_amdgcn_s_barrier();
 
-  // ---- software-pipelined token loop: wave w takes iterations w, w + NW, ...
-  // Once the K rows of its current iteration have fed the QK MFMAs it issues
-  // the K rows of its next iteration; the V rows (plus INT8 scales) follow
+  // ---- software-pipelined token loop: wave w takes chunks w, w + NW, ... of
+  // the split.  Once the K rows of its current chunk have fed the QK MFMAs it
+  // issues the K rows of its next chunk; the V rows (plus INT8 scales) follow
   // once the PV MFMAs have consumed the V registers.  HBM traffic of the next
-  // iteration overlaps this iteration's math.
-  struct Blocks {
-    int kb[PAIRS];
-    int vb[PAIRS];
-  };
-  LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
-  float ksv[PAIRS][8], vsv[PAIRS][8];   // INT8 scales of this lane's 8 tokens
-  int nvalid[PAIRS];                    // valid tokens among this lane's 8
-  // W8: K rows of tokens (t, t + 1), and the V side of an iteration: V rows
-  // of 16 tokens, the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i, and the
-  // valid tokens among the lane's 8 of each pair.
-  uint4 kw[PAIRS][KC];
-  uint4 vw[NT];
-  // W8: the scales of the 4 tokens tok0 + 16g + 4(r & 3) + i and the valid
-  // tokens among the lane's 8 of each pair.  They are loaded one iteration
-  // ahead, with the K rows, so the softmax does not wait for the V rows (the
-  // memory counter completes in order): `wa` holds the next iteration's, and
-  // each iteration copies them out before loading the following ones.
-  struct W8Buf {
-    float4 ks4, vs4;
-    int nvalid[PAIRS];
-  };
-  W8Buf wa;
-
-  // Dim-group offset (relative to the lane's group g) of k-chunk kk's K row
-  // load: 4 kk, or for the padding lanes of a 16-dim last chunk the row's
-  // last group.
-  auto kgroup = [&](int kk) { return (!KPAD || 4 * kk + g < DG) ? 4 * kk : DG - 1 - g; };
+  // chunk overlaps this chunk's math.
   auto load_blocks = [&](int it_, Blocks& b) {
-    const int tok0 = t_begin + it_ * IT;
-    if constexpr (W8) {
-      // K rows of lane (r, g) lie in the 16-token group tok0 + 16(r >> 2), its V
-      // rows and scales in tok0 + 16g; a group never straddles a block
-      // (block_size is a multiple of 16).
-      const int kg = tok0 + 16 * (r >> 2);
-      const int tg = tok0 + 16 * g;
-      const int ki = ((kg < t_end ? kg : t_begin) >> bsl) - b_first;
-      const int vi = ((tg < t_end ? tg : t_begin) >> bsl) - b_first;
-      b.kb[0] = sm.blk[ki < nblk ? ki : 0];
-      b.vb[0] = sm.blk[vi < nblk ? vi : 0];
-      return;
-    }
+    int kt[PAIRS], vt[PAIRS];
+    dw.block_tokens(t_begin + it_ * IT, t_end, t_begin, kt, vt);
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
-      const int kg = tok0 + 32 * p + 8 * (r >> 2);
-      const int tg = tok0 + 32 * p + 8 * g;
-      const int ki = ((kg < t_end ? kg : t_begin) >> bsl) - b_first;
-      const int vi = ((tg < t_end ? tg : t_begin) >> bsl) - b_first;
+      const int ki = (kt[p] >> bsl) - b_first;
+      const int vi = (vt[p] >> bsl) - b_first;
       b.kb[p] = sm.blk[ki < nblk ? ki : 0];
       b.vb[p] = sm.blk[vi < nblk ? vi : 0];
     }
   };
-  // K rows: token tok0 + 32p + 8(r>>2) + (r&3) (first MFMA) and + 4 (second).
-  auto issue_k = [&](int it_, const Blocks& b) {
-    const int tok0 = t_begin + it_ * IT;
-    if constexpr (W8) {
-      // Row r of pair p: tokens tok0 + 16(r >> 2) + 8p + 2(r & 3) and + 1.
-      const int kg = tok0 + 16 * (r >> 2);
-      const int kgc = kg < t_end ? kg : t_begin;
-      const int kb = (unsigned)b.kb[0] < (unsigned)sh.num_blocks ? b.kb[0] : 0;
-      const uint8_t* kp = kc + ((((size_t)kb * hkv + kvh) * (D / 8) + g) * bs +
-                                (kgc & (bs - 1)) + 2 * (r & 3)) * 8;
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-        for (int kk = 0; kk < KC; ++kk)
-          kw[p][kk] = load_tile<uint4, KNT>(kp + (size_t)kgroup(kk) * bs * 8 + 64 * p);
-      return;
-    }
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-      const int kg = tok0 + 32 * p + 8 * (r >> 2);
-      const int kgc = kg < t_end ? kg : t_begin;
-      const int kb = (unsigned)b.kb[p] < (unsigned)sh.num_blocks ? b.kb[p] : 0;
-      const int koff = (kgc & (bs - 1)) + (r & 3);
-      const uint8_t* kp = kc + ((((size_t)kb * hkv + kvh) * (D / 8) + g) * bs + koff) * 8 * ESZ;
-#pragma unroll
-      for (int kk = 0; kk < KC; ++kk) {
-        const uint8_t* p0 = kp + (size_t)kgroup(kk) * bs * 8 * ESZ;
-        kx[p][kk] = load_tile<LVec, KNT>(p0);
-        ky[p][kk] = load_tile<LVec, KNT>(p0 + 4 * 8 * ESZ);
-      }
-    }
-  };
-  // V rows (dims 16t + r) and the lane's score tokens tok0 + 32p + 8g .. +7.
-  // W8: the scales and valid counts of an iteration (see W8Buf).
-  auto issue_scales = [&](int it_, const Blocks& b, W8Buf& B) {
-    const int tg = t_begin + it_ * IT + 16 * g;
-    const int tgc = tg < t_end ? tg : t_begin;
-    const bool vok = (unsigned)b.vb[0] < (unsigned)sh.num_blocks;
-    const int vb = vok ? b.vb[0] : 0;
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-      const int t0 = tg + 8 * p;
-      B.nvalid[p] = (vok && t0 < t_end) ? min(8, t_end - t0) : 0;
-    }
-    const size_t slot = ((size_t)vb * hkv + kvh) * bs + (tgc & (bs - 1)) + 4 * (r & 3);
-    // (plain loads: a scale line holds several kv heads' scales)
-    B.ks4 = *reinterpret_cast<const float4*>(ksc + slot);
-    B.vs4 = *reinterpret_cast<const float4*>(vsc + slot);
-  };
-  auto issue_v = [&](int it_, const Blocks& b, W8Buf& B) {
-    const int tok0 = t_begin + it_ * IT;
-    if constexpr (W8) {
-      // V rows: dim 16t + r, tokens tok0 + 16g .. + 15 (pair p uses 8p .. 8p + 7).
-      const int tg = tok0 + 16 * g;
-      const int tgc = tg < t_end ? tg : t_begin;
-      const int vb = (unsigned)b.vb[0] < (unsigned)sh.num_blocks ? b.vb[0] : 0;
-      const uint8_t* vp = vc + (((size_t)vb * hkv + kvh) * D + r) * bs + (tgc & (bs - 1));
-#pragma unroll
-      for (int t = 0; t < NT; ++t) vw[t] = load_tile<uint4, NTL>(vp + (size_t)(16 * t) * bs);
-      return;
-    }
-#pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-      const int tg = tok0 + 32 * p + 8 * g;
-      const bool tin = tg < t_end;
-      const int tgc = tin ? tg : t_begin;
-      const bool vok = (unsigned)b.vb[p] < (unsigned)sh.num_blocks;
-      const int vb = vok ? b.vb[p] : 0;
-      const int voff = tgc & (bs - 1);
-      nvalid[p] = (tin && vok) ? min(8, t_end - tg) : 0;
-      const size_t slot = ((size_t)vb * hkv + kvh) * bs + voff;
-      const uint8_t* vp = vc + ((((size_t)vb * hkv + kvh) * D + r) * bs + voff) * ESZ;
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        vr[p][t] = load_tile<LVec, NTL>(vp + (size_t)(16 * t) * bs * ESZ);
-      if constexpr (I8) {
-        const float4 a0 = *reinterpret_cast<const float4*>(ksc + slot);
-        const float4 a1 = *reinterpret_cast<const float4*>(ksc + slot + 4);
-        const float4 b0 = *reinterpret_cast<const float4*>(vsc + slot);
-        const float4 b1 = *reinterpret_cast<const float4*>(vsc + slot + 4);
-        ksv[p][0] = a0.x; ksv[p][1] = a0.y; ksv[p][2] = a0.z; ksv[p][3] = a0.w;
-        ksv[p][4] = a1.x; ksv[p][5] = a1.y; ksv[p][6] = a1.z; ksv[p][7] = a1.w;
-        vsv[p][0] = b0.x; vsv[p][1] = b0.y; vsv[p][2] = b0.z; vsv[p][3] = b0.w;
-        vsv[p][4] = b1.x; vsv[p][5] = b1.y; vsv[p][6] = b1.z; vsv[p][7] = b1.w;
-      }
-    }
-  };
 
   // The loop is rotated so that every load inside it is unconditional: the
-  // body issues the next K, finishes the current iteration (softmax, PV),
-  // issues the next V, then runs QK of the next iteration.  The wait for K inside the body therefore never covers the V rows
-  // issued after it; the last iteration's softmax and PV run after the loop.
+  // body issues the next K, finishes the current chunk (softmax, PV), issues
+  // the next V, then runs QK of the next chunk.  The wait for K inside the
+  // body therefore never covers the V rows issued after it; the last chunk's
+  // softmax and PV run after the loop.
   if (w < n_it) {
-    auto softmax_pv = [&](float (&s)[PAIRS][8], bool need_mask, W8Buf& B) {
-      // ---- online softmax (lane-local except the per-head max)
-      float mloc = kNegInf;
-      // W8: this lane's 4 scales; token 16g + 8p + j of the lane's row is held
-      // by quad position 2p + (j >> 2), element j & 3.
-      float ksa[4] = {B.ks4.x, B.ks4.y, B.ks4.z, B.ks4.w};
-      float vsa[4] = {B.vs4.x, B.vs4.y, B.vs4.z, B.vs4.w};
-      auto nval = [&](int p) {
-        if constexpr (W8) return B.nvalid[p];
-        else return nvalid[p];
-      };
-      if constexpr (W8) {
-        if (need_mask) {
-          // the row's valid tokens are its first nvalid[0] + nvalid[1]
-          const int n16 = B.nvalid[0] + B.nvalid[1];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vsa[i] = 4 * (r & 3) + i < n16 ? vsa[i] : 0.f;
-        }
-#pragma unroll
-        for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float ksj = quad_bcast(ksa[j & 3], 2 * p + (j >> 2));
-            s[p][j] = (s[p][j] - qbias) * (ksj * c);
-          }
-      } else {
-#pragma unroll
-        for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            float v;
-            if constexpr (I8) v = (s[p][j] - qbias) * (ksv[p][j] * c);
-            else v = s[p][j] * c;
-            s[p][j] = v;
-          }
-      }
-      if (need_mask) {
-#pragma unroll
-        for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            s[p][j] = j < nval(p) ? s[p][j] : kNegInf;
-            if constexpr (I8 && !W8) vsv[p][j] = j < nval(p) ? vsv[p][j] : 0.f;
-          }
-      }
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) mloc = fmaxf(mloc, s[p][j]);
-      const float m_new = fmaxf(m_run, head_max(mloc));
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha_m = exp2f_fast(m_run - m_use);   // rescales l
-      float alpha_acc = alpha_m;                         // rescales acc (incl. weight exponent)
-      m_run = m_new;
-      float wsc;
-      if constexpr (I8) {
-        float msv = 0.f;
-        if constexpr (W8) {
-          // The 64 tokens' scales are spread over the quads of a row and the 4 rows.
-          msv = fmaxf(fmaxf(vsa[0], vsa[1]), fmaxf(vsa[2], vsa[3]));
-          msv = fmaxf(msv, dpp_mov<kQuadXor1>(msv));
-          msv = fmaxf(msv, dpp_mov<kQuadXor2>(msv));
-        } else {
-#pragma unroll
-          for (int p = 0; p < PAIRS; ++p)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) msv = fmaxf(msv, vsv[p][j]);
-        }
-        // Every head's lanes see the same tokens, so this max is wave-uniform.
-        msv = bitsf(__builtin_amdgcn_readfirstlane(fbits(head_max(msv))));
-        // Keep the weight exponent while the largest weight stays in [2^12, 2^15).
-        const float top = __builtin_amdgcn_ldexpf(msv, e_cur);
-        if (msv > 0.f && (top >= 32768.f || top < 4096.f)) {
-          int e_new = 15 - __builtin_amdgcn_frexp_expf(msv);
-          e_new = e_new < 0 ? 0 : (e_new > 30 ? 30 : e_new);
-          alpha_acc = __builtin_amdgcn_ldexpf(alpha_m, e_new - e_cur);
-          e_cur = e_new;
-        }
-        wsc = __builtin_amdgcn_ldexpf(1.f, e_cur);
-      } else {
-        wsc = 16384.f;
-      }
-      float lsum = 0.f;
-      h8_t pb[PAIRS];
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float pj = exp2f_fast(s[p][j] - m_use);
-          lsum += pj;
-          float wj;
-          if constexpr (W8) wj = pj * quad_bcast(vsa[j & 3], 2 * p + (j >> 2)) * wsc;
-          else if constexpr (I8) wj = pj * vsv[p][j] * wsc;
-          else wj = pj * wsc;
-          pb[p][j] = (half_t)wj;
-        }
-      }
-      l_part = l_part * alpha_m + lsum;
-      if (__builtin_amdgcn_ballot_w64(alpha_acc != 1.f) != 0) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] *= alpha_acc;
-      }
-
-      // ---- PV
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          h8_t av;
-          if constexpr (W8) {
-            av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y)
-                                   : make_uint2(vw[t].z, vw[t].w));
-          } else if constexpr (I8) {
-            av = i8x8_exact(vr[p][t]);
-          } else {
-            uint4 v = vr[p][t];
-            if (need_mask) v = keep_first(v, nval(p));
-            av = __builtin_bit_cast(h8_t, v);
-          }
-          acc[t] = mfma16(av, pb[p], acc[t]);
-        }
-      }
-    };
-    auto qk = [&](float (&s)[PAIRS][8]) {
-      // ---- QK: scores of tokens tok0 + 32p + 8g + j for head r (W8: tok0 + 16g + 8p + j)
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p) {
-        f4_t sx = {0.f, 0.f, 0.f, 0.f}, sy = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KC; ++kk) {
-          h8_t ax, ay;
-          if constexpr (W8) {
-            ax = i8x8_biased(make_uint2(kw[p][kk].x, kw[p][kk].y));   // token T
-            ay = i8x8_biased(make_uint2(kw[p][kk].z, kw[p][kk].w));   // token T + 1
-          } else if constexpr (I8) {
-            ax = i8x8_biased(kx[p][kk]);
-            ay = i8x8_biased(ky[p][kk]);
-          } else {
-            ax = __builtin_bit_cast(h8_t, kx[p][kk]);
-            ay = __builtin_bit_cast(h8_t, ky[p][kk]);
-          }
-          if (KPAD && kk == KC - 1 && 4 * kk + g >= DG) {
-            ax = (h8_t){};   // padding lanes of the last k-chunk (their q is zero too)
-            ay = (h8_t){};
-          }
-          sx = mfma16(ax, qreg[kk], sx);
-          sy = mfma16(ay, qreg[kk], sy);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (W8) {
-            // rows 4g + e: tokens tok0 + 16g + 8p + 2e (sx) and + 1 (sy)
-            s[p][2 * e] = sx[e];
-            s[p][2 * e + 1] = sy[e];
-          } else {
-            s[p][e] = sx[e];
-            s[p][4 + e] = sy[e];
-          }
-        }
-      }
-    };
-    auto mask_needed = [&](const W8Buf& B) {
-      // Tokens past the end or in invalid blocks exist only in the last
-      // iteration of a split (or with a corrupt block table).
-      bool short_lane = false;
-#pragma unroll
-      for (int p = 0; p < PAIRS; ++p) {
-        if constexpr (W8) short_lane = short_lane || B.nvalid[p] < 8;
-        else short_lane = short_lane || nvalid[p] < 8;
-      }
-      return __builtin_amdgcn_ballot_w64(short_lane) != 0;
-    };
     {
       Blocks b0;
       load_blocks(w, b0);
-      if constexpr (W8) issue_scales(w, b0, wa);
-      issue_k(w, b0);
+      const int tok0 = t_begin + w * IT;
+      if constexpr (W8) dw.issue_scales(cv, kvh, tok0, t_end, t_begin, b0, dw.wa);
+      dw.template issue_k<KNT>(cv, kvh, tok0, t_end, t_begin, b0);
       __builtin_amdgcn_sched_barrier(0);
-      issue_v(w, b0, wa);
+      dw.template issue_v<NTL>(cv, kvh, tok0, t_end, t_begin, b0);
       __builtin_amdgcn_sched_barrier(0);
     }
     after_issue();
-    float s[PAIRS][8];
-    qk(s);
+    float s[CT][PAIRS][8];
+    dw.qk(s);
     __builtin_amdgcn_sched_barrier(0);
     int nxt = w + NW;
-    // One iteration: the next iteration's K rows (and, W8, its scales) go out,
-    // this iteration's softmax and PV run, then the next V rows go out and
-    // the next QK runs.
+    // One iteration: the next chunk's K rows (and, W8, its scales) go out,
+    // this chunk's softmax and PV run, then the next V rows go out and the
+    // next QK runs.
     while (nxt < n_it) {
-      W8Buf cur = wa;   // W8: this iteration's scales, loaded one iteration ago
+      W8Buf cur = dw.wa;   // W8: this chunk's scales, loaded one chunk ago
       Blocks bn;
       load_blocks(nxt, bn);
-      if constexpr (W8) issue_scales(nxt, bn, wa);
-      issue_k(nxt, bn);
+      const int tok0 = t_begin + nxt * IT;
+      if constexpr (W8) dw.issue_scales(cv, kvh, tok0, t_end, t_begin, bn, dw.wa);
+      dw.template issue_k<KNT>(cv, kvh, tok0, t_end, t_begin, bn);
       __builtin_amdgcn_sched_barrier(0);
-      softmax_pv(s, mask_needed(cur), cur);
+      dw.softmax_pv(s, dw.mask_needed(cur), cur, c);
       __builtin_amdgcn_sched_barrier(0);
-      issue_v(nxt, bn, wa);
+      dw.template issue_v<NTL>(cv, kvh, tok0, t_end, t_begin, bn);
       __builtin_amdgcn_sched_barrier(0);
-      qk(s);
+      dw.qk(s);
       __builtin_amdgcn_sched_barrier(0);
       nxt += NW;
     }
-    softmax_pv(s, mask_needed(wa), wa);
+    dw.softmax_pv(s, dw.mask_needed(dw.wa), dw.wa, c);
   } else {
     after_issue();
   }
 
-  // ---- per-wave results: m (head r), l, acc (dims 16t + 4g + e)
-  float l_run = head_sum(l_part);
-  const float unscale = __builtin_amdgcn_ldexpf(1.f, -e_cur);
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] *= unscale;
-
-  // ---- every wave's state goes to LDS; then each thread merges the NW
-  // states of its (head, 4-dim chunk) items and writes them out: the output
-  // when the unit has one split, else this split's partial.
-  if (r < gt) {
-    if (g == 0) {
-      sm.m[w][r] = m_run;
-      sm.l[w][r] = l_run;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      *reinterpret_cast<f4_t*>(&sm.a[w][r][16 * t + 4 * g]) = acc[t];
-  }
-  __syncthreads();
-
-  constexpr int CH = D / 4;
+  // ---- per-wave results, column tile by column tile: every wave's state
+  // goes to LDS; then the work-group's threads merge them and write the
+  // output when the unit has one split, else this split's partial.
   const size_t out_base = ((size_t)seq * sh.num_heads + head0) * D;
   const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
   const size_t slot = wk.slot0 + (size_t)split * wk.stride;
   const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
   const auto rml = buf_rsrc(pml + slot * gt * 2, (uint32_t)(gt * 8));
-  for (int i = tid; i < gt * CH; i += NW * kWave) {
-    const int h = i / CH, c = i - h * CH;
-    float mw[NW], M = kNegInf;
 #pragma unroll
-    for (int v = 0; v < NW; ++v) {
-      mw[v] = sm.m[v][h];
-      M = fmaxf(M, mw[v]);
-    }
-    f4_t A = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
-#pragma unroll
-    for (int v = 0; v < NW; ++v) {
-      const float f = mw[v] == kNegInf ? 0.f : exp2f_fast(mw[v] - M);
-      L += sm.l[v][h] * f;
-      A += *reinterpret_cast<const f4_t*>(&sm.a[v][h][4 * c]) * f;
-    }
-    if (final_here) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      const uint2 pk = make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
-      *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
-    } else {
-      // FUSED: device-coherent (write-through) stores, visible to every XCD
-      // once this thread's stores are acknowledged.
-      constexpr int POL = FUSED ? kPolicyDevice : 0;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc,
-                                             (h * D + 4 * c) * 4, 0, POL);
-      if (c == 0) {
-        const f2_t ml = {M, L};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml), rml, h * 8, 0, POL);
-      }
-    }
+  for (int ct = 0; ct < CT; ++ct) {
+    const int nh = min(16, gt - 16 * ct);   // query heads of this tile
+    if (ct > 0) __syncthreads();            // the previous tile's merge has read its slots
+    dw.store_state(sm, w, ct, nh);
+    __syncthreads();
+    merge_wave_states<D, NW, FUSED>(sm, ct, nh, tid, final_here, out, out_base, racc, rml);
   }
   if constexpr (FUSED) {
     if (ns_eff > 1) {
@@ -787,8 +967,10 @@ __device__ __forceinline__ void decode_split(
       }
       __syncthreads();
       if (sm.last) {
-        merge_splits<D, NW * kWave, true>(pacc, pml, out, wk.slot0, wk.stride, gt, out_base,
-                                          ns_eff);
+        const size_t slot0 = wk.slot0, stride = wk.stride;
+        merge_splits<D, NW * kWave, true>(
+            pacc, pml, out, [=](int sp) { return slot0 + (size_t)sp * stride; }, gt, out_base,
+            ns_eff);
         if (threadIdx.x == 0)
           __hip_atomic_store(cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -819,7 +1001,7 @@ __device__ __forceinline__ void decode_split(
   sh.num_blocks = sh_num_blocks
 
 // Grid form: one work-group per (unit, split) slot of the host's plan.
-template <int D, int NW, bool I8, bool FUSED, bool NTL, bool KNT>
+template <int D, int NW, int CT, bool I8, bool FUSED, bool NTL, bool KNT>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE_HEAD_PARAMS,
               DecodeShape sh_tail, const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
@@ -878,7 +1060,7 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
     return split < ns;
   };
-  decode_split<D, NW, I8, FUSED, false, NTL, KNT>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
+  decode_split<D, NW, CT, I8, FUSED, false, NTL, KNT>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
                                              sm, resolve, [] {});
 }
 
@@ -1082,7 +1264,7 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
   return sc;
 }
 
-template <int D, int NW, bool I8, bool FUSED, bool NTL>
+template <int D, int NW, int CT, bool I8, bool FUSED, bool NTL>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                     PA_SHAPE_HEAD_PARAMS, DecodeShape sh_tail, const half_t* __restrict__ q,
@@ -1147,7 +1329,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                                  : split * P + __builtin_amdgcn_readfirstlane((int)ss.rem[seq]);
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
-    decode_split<D, NW, I8, FUSED, true, NTL, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
+    decode_split<D, NW, CT, I8, FUSED, true, NTL, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
                                               wk, sm, [](int&, int&) { return true; }, claim);
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
@@ -1191,9 +1373,276 @@ sched_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pm
   if (rb < 0 || rb > rows_max - ns) return;   // slots stay inside the partial buffers
   const size_t rowbase = (size_t)rb;
   const int head0 = kvh * sh.group + chunk * sh.head_tile;
+  const size_t slot0 = (rowbase * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
+  const size_t stride = (size_t)sh.num_kv_heads * sh.nchunk;
   merge_splits<D, kThreads, false>(
-      pacc, pml, out, (rowbase * sh.num_kv_heads + kvh) * sh.nchunk + chunk,
-      sh.num_kv_heads * sh.nchunk, sh.head_tile, ((size_t)seq * sh.num_heads + head0) * D, ns);
+      pacc, pml, out, [=](int sp) { return slot0 + (size_t)sp * stride; }, sh.head_tile,
+      ((size_t)seq * sh.num_heads + head0) * D, ns);
+}
+
+// ---------------------------------------------------------------------------
+// Stream partition (split-K kinds): every (sequence, kv head, head chunk)
+// is a stream of IT-token chunks.  The streams of all sequences, in
+// sequence order, form one list of N chunks, and work-group b of the G
+// launched takes the contiguous range [b N / G, (b + 1) N / G): every
+// work-group gets the same number of chunks, whatever the spread of the
+// lengths, and no chunk is tied to a split boundary.  The waves of a
+// work-group deal the range's chunks round-robin and stream through them with
+// one software pipeline that does not stop at stream boundaries: the block
+// ids of a wave's chunk after next are loaded while it works on the current
+// one, and the K/V rows of its next chunk are in flight whatever stream that
+// chunk belongs to.  Where the range's part of a stream ends, the waves merge
+// their states through LDS: a stream that lies wholly inside the range gets
+// its output written there; otherwise the part becomes one of the range's
+// two partials (slot 2b for the part that starts the range, 2b + 1 for the
+// one that ends it), which stream_reduce_kernel merges.
+
+struct StreamSmemTail {
+  int pre[kSchedMaxSeqs + 1];   // chunks of all streams of the sequences before s
+  int ctx[kSchedMaxSeqs];       // context length of s (clamped)
+  int scan[16];                 // per-wave totals of the prefix scan
+};
+
+template <int D, int NW>
+struct alignas(16) StreamSmem {
+  float a[NW][16][D + kMergeRowPad];   // each wave's accumulator: per head, per dim (+ pad)
+  float m[NW][16];
+  float l[NW][16];
+  StreamSmemTail t;
+};
+
+// Position of global chunk x: sequence s, stream u of s (kv head u / nchunk,
+// head chunk u % nchunk), chunk c of the stream; the stream holds nch chunks
+// and ends before global chunk `end`.  Work-group uniform.
+struct ChunkPos {
+  int x, s, u, c, nch, end, ctx;
+};
+
+__device__ __forceinline__ ChunkPos locate_chunk(const StreamSmemTail& t, int S, int U, int x) {
+  ChunkPos z;
+  z.x = x;
+  z.s = __builtin_amdgcn_readfirstlane(prefix_search(t.pre, S, x));
+  const int p0 = __builtin_amdgcn_readfirstlane(t.pre[z.s]);
+  z.nch = __builtin_amdgcn_readfirstlane((t.pre[z.s + 1] - p0) / U);
+  const int off = x - p0;
+  z.u = off / z.nch;
+  z.c = off - z.u * z.nch;
+  z.end = p0 + (z.u + 1) * z.nch;
+  z.ctx = __builtin_amdgcn_readfirstlane(t.ctx[z.s]);
+  return z;
+}
+
+// The chunk `by` places further on (x + by < N).
+__device__ __forceinline__ ChunkPos advance_chunk(const StreamSmemTail& t, int S, int U,
+                                                  const ChunkPos& z, int by) {
+  if (z.x + by < z.end) {
+    ChunkPos n = z;
+    n.x += by;
+    n.c += by;
+    return n;
+  }
+  return locate_chunk(t, S, U, z.x + by);
+}
+
+// Per-sequence chunk counts (ceil(ctx / IT) for each of the U streams) and
+// their exclusive prefix over the sequences; returns N, the total.
+template <int NTH, int IT>
+__device__ int stream_prefix(const int* __restrict__ ctxl, int S, int U, int cap,
+                             StreamSmemTail& t) {
+  constexpr int E = (kSchedMaxSeqs + NTH - 1) / NTH;
+  constexpr int NWV = NTH / kWave;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & (kWave - 1);
+  int c[E], n[E], sum = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid * E + e;
+    int v = i < S ? ctxl[i] : 0;
+    v = v < 0 ? 0 : (v > cap ? cap : v);
+    c[e] = v;
+    n[e] = (v + IT - 1) / IT * U;
+    sum += n[e];
+  }
+  const int incl = wave_scan_i(sum);
+  if (lane == kWave - 1) t.scan[w] = incl;
+  __syncthreads();
+  int off = incl - sum, total = 0;
+#pragma unroll
+  for (int i = 0; i < NWV; ++i) {
+    const int v = t.scan[i];
+    if (i < w) off += v;
+    total += v;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid * E + e;
+    if (i < S) {
+      t.pre[i] = off;
+      t.ctx[i] = c[e];
+      off += n[e];
+    }
+  }
+  if (tid == 0) t.pre[S] = total;
+  __syncthreads();
+  return total;
+}
+
+template <int D, int NW, int CT, bool I8, bool NTL>
+__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+decode_stream_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
+                     PA_SHAPE_HEAD_PARAMS, DecodeShape sh_tail, const half_t* __restrict__ q,
+                     const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
+                     const float* __restrict__ ksc, const float* __restrict__ vsc,
+                     half_t* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
+                     int* __restrict__ info) {
+  PA_SHAPE_REBUILD(sh, sh_tail);
+  using Wave = DecodeWave<D, CT, I8>;
+  using Blocks = typename Wave::Blocks;
+  using W8Buf = typename Wave::W8Buf;
+  constexpr int PAIRS = Wave::PAIRS;
+  constexpr int IT = Wave::IT;
+  constexpr bool W8 = Wave::W8;
+  static_assert(sizeof(StreamSmem<D, NW>) * (kWavesPerCU / NW) <= kLdsPerCU, "LDS budget");
+  __shared__ StreamSmem<D, NW> sm;
+
+  const int S = sh.num_seqs, U = sh.num_kv_heads * sh.nchunk, gt = sh.head_tile;
+  const int N = stream_prefix<NW * kWave, IT>(ctxl, S, U, sh.max_blocks * sh.block_size, sm.t);
+  // The reduce reads N and the prefix.
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i <= S; i += NW * kWave) info[1 + i] = sm.t.pre[i];
+    if (threadIdx.x == 0) info[0] = N;
+  }
+  // With fewer chunks than work-groups, the first N take one each.
+  const int G = min((int)gridDim.x, N);
+  if ((int)blockIdx.x >= G) return;
+  const int A = (int)((long long)blockIdx.x * N / G);
+  const int B = (int)((long long)(blockIdx.x + 1) * N / G);
+
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int bsl = sh.bs_log2;
+  const CacheView cv{kc, vc, ksc, vsc, sh.num_kv_heads, sh.block_size, sh.num_blocks};
+  const float c = sh.scale_log2;
+  Wave dw;
+  dw.init(lane);
+
+  // Block ids of chunk z for this lane's loads, from the block table.
+  auto chunk_blocks = [&](const ChunkPos& z, Blocks& b) {
+    int kt[PAIRS], vt[PAIRS];
+    const int tok0 = z.c * IT;
+    dw.block_tokens(tok0, z.ctx, tok0, kt, vt);
+    const int* row = bt + (size_t)z.s * sh.max_blocks;
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      b.kb[p] = row[kt[p] >> bsl];
+      b.vb[p] = row[vt[p] >> bsl];
+    }
+  };
+  auto kv_head = [&](const ChunkPos& z) { return z.u / sh.nchunk; };
+
+  // Wave w's chunks are A + w, A + w + NW, ... below B.  A wave without a next
+  // chunk keeps loading its last one (every load of the loop is
+  // unconditional, so the waits inside it never cover a later load).
+  const bool have = w < B - A;
+  ChunkPos cur = locate_chunk(sm.t, S, U, have ? A + w : A);
+  ChunkPos nxt = (cur.x + NW < B) ? advance_chunk(sm.t, S, U, cur, NW) : cur;
+  // The loads go out in the loop's order: K rows, then the next block ids,
+  // then V rows.
+  Blocks bn;
+  {
+    Blocks b0;
+    chunk_blocks(cur, b0);
+    const int tok0 = cur.c * IT;
+    if constexpr (W8) dw.issue_scales(cv, kv_head(cur), tok0, cur.ctx, tok0, b0, dw.wa);
+    dw.template issue_k<false>(cv, kv_head(cur), tok0, cur.ctx, tok0, b0);
+    const typename Wave::VPlan vplan = dw.plan_v(cv, kv_head(cur), tok0, cur.ctx, tok0, b0);
+    chunk_blocks(nxt, bn);
+    __builtin_amdgcn_sched_barrier(0);
+    dw.template issue_v<NTL>(cv, vplan);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  for (int seg_lo = A; seg_lo < B;) {
+    // The range's part of one stream: [seg_lo, seg_hi).
+    const ChunkPos sg = locate_chunk(sm.t, S, U, seg_lo);
+    const int seg_hi = min(B, sg.end);
+    const bool whole = seg_lo == sg.end - sg.nch && seg_hi == sg.end;
+    const int kvh = kv_head(sg), chunk = sg.u - kvh * sh.nchunk;
+    const int head0 = kvh * sh.group + chunk * gt;
+    dw.load_q(q, (size_t)sg.s * sh.num_heads + head0, gt);
+    dw.compute_qbias();
+    dw.reset();
+    while (have && cur.x < seg_hi) {
+      float s[CT][PAIRS][8];
+      dw.qk(s);
+      __builtin_amdgcn_sched_barrier(0);
+      // The next chunk's K rows (and, W8, its scales) go out; then the block
+      // ids of the one after it, into the registers those rows came from.
+      W8Buf curw = dw.wa;   // W8: this chunk's scales, loaded one chunk ago
+      const int ntok0 = nxt.c * IT, nkvh = kv_head(nxt);
+      if constexpr (W8) dw.issue_scales(cv, nkvh, ntok0, nxt.ctx, ntok0, bn, dw.wa);
+      dw.template issue_k<false>(cv, nkvh, ntok0, nxt.ctx, ntok0, bn);
+      const typename Wave::VPlan vplan = dw.plan_v(cv, nkvh, ntok0, nxt.ctx, ntok0, bn);
+      const ChunkPos after = (nxt.x + NW < B) ? advance_chunk(sm.t, S, U, nxt, NW) : nxt;
+      chunk_blocks(after, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      dw.softmax_pv(s, dw.mask_needed(curw), curw, c);
+      __builtin_amdgcn_sched_barrier(0);
+      dw.template issue_v<NTL>(cv, vplan);
+      __builtin_amdgcn_sched_barrier(0);
+      // past the wave's last chunk the position stays beyond the range
+      cur = (nxt.x != cur.x) ? nxt : ChunkPos{B, 0, 0, 0, 1, B + 1, 0};
+      nxt = after;
+    }
+    // ---- the part's end: every wave's state (empty for a wave without a
+    // chunk in it) merges through LDS, column tile by column tile.
+    const size_t out_base = ((size_t)sg.s * sh.num_heads + head0) * D;
+    const size_t slot = 2 * (size_t)blockIdx.x + (seg_lo == A ? 0 : 1);
+    const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
+    const auto rml = buf_rsrc(pml + slot * gt * 2, (uint32_t)(gt * 8));
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int nh = min(16, gt - 16 * ct);
+      __syncthreads();   // the previous merge has read the slots
+      dw.store_state(sm, w, ct, nh);
+      __syncthreads();
+      merge_wave_states<D, NW, false>(sm, ct, nh, tid, whole, out, out_base, racc, rml);
+    }
+    seg_lo = seg_hi;
+  }
+}
+
+// Merge of the streams the stream partition split between work-groups: one
+// work-group per (sequence, stream); a stream inside one work-group's range
+// was written by it, a sequence without tokens gets zeros.
+template <int D>
+__global__ void __launch_bounds__(kThreads)
+stream_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
+                     const int* __restrict__ info, half_t* __restrict__ out, DecodeShape sh,
+                     int groups) {
+  const int U = sh.num_kv_heads * sh.nchunk;
+  const int s = blockIdx.x / U, u = blockIdx.x - s * U;
+  const int kvh = u / sh.nchunk, chunk = u - kvh * sh.nchunk;
+  const int gt = sh.head_tile;
+  const size_t out_base = ((size_t)s * sh.num_heads + kvh * sh.group + chunk * gt) * D;
+  const int N = info[0], p0 = info[1 + s], p1 = info[2 + s];
+  const int nch = (p1 - p0) / U;
+  if (nch <= 0) {
+    for (int i = threadIdx.x; i < gt * D / 4; i += kThreads)
+      *reinterpret_cast<uint2*>(out + out_base + 4 * (size_t)i) = make_uint2(0, 0);
+    return;
+  }
+  const long long G = min(groups, N);
+  const long long x0 = p0 + (long long)u * nch, x1 = x0 + nch;
+  // work-group of chunk x: the last one whose range starts at or before x
+  auto group_of = [&](long long x) { return (int)(((x + 1) * G - 1) / N); };
+  const int g0 = group_of(x0), g1 = group_of(x1 - 1);
+  if (g0 == g1) return;
+  const size_t first = 2 * (size_t)g0 + ((long long)g0 * N / G == x0 ? 0 : 1);
+  merge_splits<D, kThreads, false>(
+      pacc, pml, out, [=](int k) { return k == 0 ? first : 2 * (size_t)(g0 + k); }, gt, out_base,
+      g1 - g0 + 1);
 }
 
 // Split-K reduce: one work-group per (seq, kv_head, head chunk).
@@ -1211,11 +1660,13 @@ splitk_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ p
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int ns_eff = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
   const int head0 = kvh * sh.group + chunk * sh.head_tile;
-  merge_splits<D, kThreads, false>(pacc, pml, out, (size_t)unit * sh.nsplit, 1, sh.head_tile,
-                                   ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
+  const size_t slot0 = (size_t)unit * sh.nsplit;
+  merge_splits<D, kThreads, false>(
+      pacc, pml, out, [=](int sp) { return slot0 + (size_t)sp; }, sh.head_tile,
+      ((size_t)seq * sh.num_heads + head0) * D, ns_eff);
 }
 
-template <int D, int NW, bool I8, bool NTL, bool KNT>
+template <int D, int NW, int CT, bool I8, bool NTL, bool KNT>
 hipError_t launch_decode_grid(const DecodeLaunch& l, int grid) {
   const DecodeShape& sh = l.shape;
   const auto* q = static_cast<const half_t*>(l.q);
@@ -1223,12 +1674,12 @@ hipError_t launch_decode_grid(const DecodeLaunch& l, int grid) {
   const auto* vc = static_cast<const uint8_t*>(l.v_cache);
   auto* out = static_cast<half_t*>(l.out);
   if (l.fused) {
-    decode_kernel<D, NW, I8, true, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
+    decode_kernel<D, NW, CT, I8, true, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
         l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
         l.part_ml, l.counters);
     return hipGetLastError();
   }
-  decode_kernel<D, NW, I8, false, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
+  decode_kernel<D, NW, CT, I8, false, NTL, KNT><<<grid, NW * kWave, 0, l.stream>>>(
       l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
       l.part_ml, l.counters);
   hipError_t e = hipGetLastError();
@@ -1239,9 +1690,24 @@ hipError_t launch_decode_grid(const DecodeLaunch& l, int grid) {
   return hipGetLastError();
 }
 
-template <int D, int NW, bool I8, bool NTL>
-hipError_t launch_decode_waves(const DecodeLaunch& l) {
+template <int D, int NW, int CT, bool I8, bool NTL>
+hipError_t launch_decode_tiles(const DecodeLaunch& l) {
   const DecodeShape& sh = l.shape;
+  if (l.stream_part) {
+    const auto* q = static_cast<const half_t*>(l.q);
+    const auto* kc = static_cast<const uint8_t*>(l.k_cache);
+    const auto* vc = static_cast<const uint8_t*>(l.v_cache);
+    auto* out = static_cast<half_t*>(l.out);
+    decode_stream_kernel<D, NW, CT, I8, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
+        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales,
+        l.v_scales, out, l.part_acc, l.part_ml, l.sched_info);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int streams = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
+    stream_reduce_kernel<D><<<streams, kThreads, 0, l.stream>>>(l.part_acc, l.part_ml,
+                                                                  l.sched_info, out, sh, l.groups);
+    return hipGetLastError();
+  }
   if (l.sched) {
     const SchedArgs sa{l.sched_info, l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform};
     const auto* q = static_cast<const half_t*>(l.q);
@@ -1249,12 +1715,12 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
     const auto* vc = static_cast<const uint8_t*>(l.v_cache);
     auto* out = static_cast<half_t*>(l.out);
     if (l.fused) {
-      decode_sched_kernel<D, NW, I8, true, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
+      decode_sched_kernel<D, NW, CT, I8, true, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
           l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
           l.part_ml, l.counters, sa);
       return hipGetLastError();
     }
-    decode_sched_kernel<D, NW, I8, false, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
+    decode_sched_kernel<D, NW, CT, I8, false, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
         l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
         l.part_ml, l.counters, sa);
     hipError_t e = hipGetLastError();
@@ -1269,10 +1735,20 @@ hipError_t launch_decode_waves(const DecodeLaunch& l) {
   const int grid = sh.num_items >= 8
                        ? (sh.num_items + 7) / 8 * 8 * sh.num_kv_heads * sh.nchunk
                        : (sh.num_items * sh.num_kv_heads + 7) / 8 * 8 * sh.nchunk;
-  if constexpr (!I8 && NTL) {
-    if (l.k_nt) return launch_decode_grid<D, NW, I8, NTL, true>(l, grid);
+  if constexpr (!I8 && NTL && CT == 1) {
+    if (l.k_nt) return launch_decode_grid<D, NW, CT, I8, NTL, true>(l, grid);
   }
-  return launch_decode_grid<D, NW, I8, NTL, false>(l, grid);
+  return launch_decode_grid<D, NW, CT, I8, NTL, false>(l, grid);
+}
+
+// Two MFMA column tiles when a work-group serves more than 16 query heads
+// (head_dim <= 128; the planner keeps head tiles of head_dim 256 at 16).
+template <int D, int NW, bool I8, bool NTL>
+hipError_t launch_decode_waves(const DecodeLaunch& l) {
+  if constexpr (D <= 128) {
+    if (l.shape.head_tile > kMaxGroupTile) return launch_decode_tiles<D, NW, 2, I8, NTL>(l);
+  }
+  return launch_decode_tiles<D, NW, 1, I8, NTL>(l);
 }
 
 template <int D, bool I8, bool NTL>
@@ -1293,36 +1769,46 @@ hipError_t launch_decode_d(const DecodeLaunch& l) {
   return l.int8_kv ? launch_decode_dtype<D, true>(l) : launch_decode_dtype<D, false>(l);
 }
 
-// Resident work-groups of the scheduled kernel for one head_dim (cached per
-// device and variant).
+// Resident work-groups of the persistent decode kernels for one head_dim
+// (cached per device and variant): the in-kernel schedule (stream_part =
+// false) or the stream partition.
+template <int D, int NW, int CT>
+int resident_query(bool int8_kv, bool stream_part, int* per_cu) {
+  hipError_t e;
+  if (stream_part)
+    e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      per_cu, decode_stream_kernel<D, NW, CT, true, true>, NW * kWave, 0)
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      per_cu, decode_stream_kernel<D, NW, CT, false, true>, NW * kWave, 0);
+  else
+    e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      per_cu, decode_sched_kernel<D, NW, CT, true, true, true>, NW * kWave, 0)
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      per_cu, decode_sched_kernel<D, NW, CT, false, true, true>, NW * kWave, 0);
+  return e == hipSuccess ? 0 : -1;
+}
+
 template <int D>
-int sched_groups_d(int waves, bool int8_kv) {
-  static int cache[64][4] = {};
+int resident_groups_d(bool stream_part, int waves, bool int8_kv, int column_tiles) {
+  static int cache[64][16] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   const int nw = (D <= 128 && waves == 8) ? 8 : 4;
-  const int slot = (nw == 8 ? 2 : 0) + (int8_kv ? 1 : 0);
+  const int ct = (D <= 128 && column_tiles == 2) ? 2 : 1;
+  const int slot = (stream_part ? 8 : 0) + (ct == 2 ? 4 : 0) + (nw == 8 ? 2 : 0) + (int8_kv ? 1 : 0);
   if (cache[dev][slot] == 0) {
-    int cus = 0, per_cu = 0;
+    int cus = 0, per_cu = 0, e = -1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    hipError_t e;
-    if (nw == 8) {
-      if constexpr (D <= 128) {
-        e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                          &per_cu, decode_sched_kernel<D, 8, true, true, true>, 8 * kWave, 0)
-                    : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                          &per_cu, decode_sched_kernel<D, 8, false, true, true>, 8 * kWave, 0);
-      } else {
-        e = hipErrorInvalidValue;
-      }
+    if constexpr (D <= 128) {
+      if (nw == 8) e = ct == 2 ? resident_query<D, 8, 2>(int8_kv, stream_part, &per_cu)
+                               : resident_query<D, 8, 1>(int8_kv, stream_part, &per_cu);
+      else e = ct == 2 ? resident_query<D, 4, 2>(int8_kv, stream_part, &per_cu)
+                       : resident_query<D, 4, 1>(int8_kv, stream_part, &per_cu);
     } else {
-      e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                        &per_cu, decode_sched_kernel<D, 4, true, true, true>, 4 * kWave, 0)
-                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                        &per_cu, decode_sched_kernel<D, 4, false, true, true>, 4 * kWave, 0);
+      e = resident_query<D, 4, 1>(int8_kv, stream_part, &per_cu);
     }
-    if (e != hipSuccess || per_cu <= 0 || cus <= 0) return 0;
+    if (e != 0 || per_cu <= 0 || cus <= 0) return 0;
     cache[dev][slot] = cus * per_cu;
   }
   return cache[dev][slot];

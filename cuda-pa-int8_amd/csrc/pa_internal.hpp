@@ -11,7 +11,10 @@
 namespace pa {
 
 constexpr int kIterTokens = 64;      // partition granularity (one wave iteration for head_dim <= 128)
-constexpr int kMaxGroupTile = 16;    // query heads sharing one KV read (one MFMA column tile)
+constexpr int kMaxGroupTile = 16;    // query heads of one MFMA column tile
+// Query heads one work-group serves for head_dim <= 128: two column tiles,
+// so that each K/V load feeds up to 32 heads (MQA 32/1 in one work-group).
+constexpr int kMaxHeadTile = 32;
 // Largest split, per 4 waves of a work-group.  The planner never exceeds it
 // (forced partitions included), so the block ids of one split fit in LDS.
 // 8192 rather than 4096 for head_dim <= 128: uniform long contexts get half
@@ -70,13 +73,18 @@ struct DecodeLaunch {
   bool k_nt;           // non-temporal K-row loads too (FP16 grid launches, long splits)
   DecodeShape shape;
   // In-kernel schedule (sched = true): `groups` resident work-groups claim
-  // (row, kv head) items; the partials hold `rows_max` slot rows.
+  // (row, kv head) items; the partials hold `rows_max` slot rows.  Stream
+  // partition (stream_part = true): `groups` work-groups take equal
+  // contiguous ranges of the chunk list; the partials hold 2 * groups slots
+  // and sched_info receives the chunk prefix.
   bool sched;
+  bool stream_part;
   int groups;
   int rows_max;
   int pmin, pmax;      // partition bounds, multiples of 64 (equal when forced)
   int pmin_uniform;    // lower bound for equal lengths (<= pmin)
-  int* sched_info;     // [1 + num_seqs]: partition, then the slot row base of each sequence
+  int* sched_info;     // schedule: [1 + num_seqs] partition, then the slot row base of each
+                       // sequence; stream partition: [2 + num_seqs] chunk total, then prefix
   uint32_t* queue;     // 8 claim counters, zero between launches
   hipStream_t stream;
 };
@@ -123,10 +131,12 @@ pa_status_t decode_launch_capped(const DecodeCall& c, void* counters, size_t cou
 #define PA_FOR_EACH_HEAD_DIM(X) X(64) X(80) X(96) X(112) X(128) X(256)
 
 // Per head_dim D: the launcher of every decode kind, and the resident
-// work-groups of the scheduled decode kernel (0 if it cannot run).
-#define PA_DECLARE_DECODE_D(D)                               \
-  hipError_t launch_decode_d##D(const DecodeLaunch& l);      \
-  int sched_groups_d##D(int waves, bool int8_kv);
+// work-groups of a persistent decode kernel (the in-kernel schedule, or the
+// stream partition) for a wave count and 1 or 2 column tiles (0 if it
+// cannot run).
+#define PA_DECLARE_DECODE_D(D)                                                          \
+  hipError_t launch_decode_d##D(const DecodeLaunch& l);                                 \
+  int resident_groups_d##D(bool stream_part, int waves, bool int8_kv, int column_tiles);
 PA_FOR_EACH_HEAD_DIM(PA_DECLARE_DECODE_D)
 #undef PA_DECLARE_DECODE_D
 

@@ -89,6 +89,7 @@ PROTOTYPES = {
     "pa_decode_set_waves_per_group": (ctypes.c_int, [_i32]),
     "pa_decode_set_schedule": (ctypes.c_int, [_i32]),
     "pa_decode_set_load_policy": (ctypes.c_int, [_i32]),
+    "pa_decode_set_max_head_tile": (ctypes.c_int, [_i32]),
     "pa_paged_decode_attn_warp": (ctypes.c_int, _DECODE_F16_ARGS),
     "pa_paged_decode_attn_splitk": (ctypes.c_int, _DECODE_F16_ARGS),
     "pa_paged_decode_attn_warp_int8": (ctypes.c_int, _DECODE_I8_ARGS),

@@ -30,8 +30,14 @@ pa_status_t pa_decode_set_waves_per_group(int32_t waves);
  * work-group per (unit, split) slot of the host plan; 2 = in-kernel schedule:
  * persistent work-groups, one per resident slot, claim (split, kv head, head
  * chunk) items of a compact work list that every work-group derives from
- * context_lens. */
+ * context_lens; 3 = stream partition (split-K kinds, up to 1024 sequences):
+ * the chunks of all (sequence, kv head) streams form one list, and every
+ * resident work-group takes an equal contiguous range of it. */
 pa_status_t pa_decode_set_schedule(int32_t mode);
+
+/* The most query heads one work-group serves: 16 or 32 (two MFMA column
+ * tiles, head_dim <= 128 only); 0 restores the automatic choice. */
+pa_status_t pa_decode_set_max_head_tile(int32_t heads);
 
 /* Cache hint of the V-row loads (K rows load plain, except in FP16 grid
  * launches whose splits hold at least 4096 tokens, which follow V).

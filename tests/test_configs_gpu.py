@@ -168,11 +168,12 @@ def test_config4_single_launch(variant):
 
 @pytest.mark.parametrize("hkv", [8, 1])
 @pytest.mark.parametrize("variant", ["splitk", "splitk_int8"])
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 def test_config5_ragged_mix(hkv, variant, mode):
     """Config 5: 256 sequences, lognormal(ln 1024, 1.0) lengths clipped to
     [16, 32768] (seed 5, as bench.py), 32 q heads over 8 kv heads or MQA 32/1,
-    on the host grid (mode 1) and the in-kernel schedule (mode 2); 24
+    on the host grid (mode 1), the in-kernel schedule (mode 2) and the stream
+    partition (mode 3); 24
     sequences checked, the longest and the shortest among them."""
     import pa_int8
 

@@ -176,6 +176,46 @@ def test_fp16_group_sizes(variant, num_heads, num_kv_heads):
     assert_close(run_fp16(c, variant), oracle_fp16(c), what=f"{variant} {num_heads}/{num_kv_heads}")
 
 
+@pytest.mark.parametrize("variant", F16_VARIANTS + I8_VARIANTS)
+@pytest.mark.parametrize("num_heads,num_kv_heads", [(32, 1), (17, 1), (40, 2), (24, 1),
+                                                    (64, 1), (96, 2)])
+@pytest.mark.parametrize("mode", [1, 2, 3])
+def test_two_column_tiles(variant, num_heads, num_kv_heads, mode):
+    """Group sizes of 17..32 query heads run in one work-group per kv head with
+    two MFMA column tiles (64/1 and 96/2: two such chunks of 32 and 48 = 24+24);
+    ragged lengths, grid (mode 1), in-kernel schedule (mode 2; 16-head tiles)
+    and stream partition (mode 3), default and
+    forced short partitions (many-split merges)."""
+    import pa_int8
+
+    lib = pa_int8.capi()
+    lens = np.array([1, 333, 2100, 17], np.int32)
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(4, lens, num_heads, num_kv_heads, seed=num_heads)
+    want = oracle_int8(c) if int8 else oracle_fp16(c)
+    run = run_int8 if int8 else run_fp16
+    try:
+        assert lib.pa_decode_set_schedule(mode) == 0
+        for part in (0, 128):
+            assert_close(run(c, variant, partition=part), want,
+                         what=f"{variant} {num_heads}/{num_kv_heads} mode {mode} P={part}")
+    finally:
+        lib.pa_decode_set_schedule(0)
+
+
+@pytest.mark.parametrize("head_dim", [64, 80, 96, 112, 256])
+@pytest.mark.parametrize("variant", ["warp", "splitk_int8"])
+def test_two_column_tiles_head_dims(head_dim, variant):
+    """MQA 32/1 at every head_dim: two column tiles up to 128, two 16-head
+    chunks at 256."""
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(3, make_lens(900, 3), 32, 1, head_dim=head_dim,
+                                           seed=head_dim)
+    got = run_int8(c, variant) if int8 else run_fp16(c, variant)
+    assert_close(got, oracle_int8(c) if int8 else oracle_fp16(c),
+                 what=f"{variant} 32/1 D={head_dim}")
+
+
 def test_fp16_qwen_config_full_size():
     """BASELINE config 2 at its real size: 32 seqs x 4096, 12/2 heads, D=128."""
     c = fp16_case(32, np.full(32, 4096, dtype=np.int32), 12, 2, seed=2)

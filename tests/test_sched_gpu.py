@@ -1,12 +1,14 @@
-"""GPU tests of the two work distributions of the decode kernels.
+"""GPU tests of the three work distributions of the decode kernels.
 
 ``pa_decode_set_schedule`` selects the grid form (one work-group per
-(unit, split) slot of the host plan) or the in-kernel schedule (persistent
-work-groups over a compact work list built from context_lens on the device).
-Both must give the oracle's result on ragged batches, capacity-sized block
-tables, many sequences and zero-length sequences; the schedule's claim
-counters must return to zero after every launch (checked by running
-different shapes back to back); results are bitwise reproducible.
+(unit, split) slot of the host plan), the in-kernel schedule (persistent
+work-groups over a compact work list built from context_lens on the device)
+or the stream partition (split-K kinds: every resident work-group takes an
+equal contiguous range of all streams' chunks; the single-launch kinds run
+the grid under it).  All must give the oracle's result on ragged batches,
+capacity-sized block tables, many sequences and zero-length sequences; the
+schedule's claim counters must return to zero after every launch (checked by
+running different shapes back to back); results are bitwise reproducible.
 """
 
 import math
@@ -19,7 +21,7 @@ from _cases import assert_close, fp16_case, int8_case, oracle_fp16, oracle_int8
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-GRID, SCHED = 1, 2
+GRID, SCHED, STREAM = 1, 2, 3
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -65,7 +67,7 @@ def run(c, variant, lens=None, bt=None, check=True, int8=False, partition=0):
     return out.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp", "splitk"])
 @pytest.mark.parametrize("heads", [(16, 8), (12, 2), (32, 1)])
 def test_ragged_fp16(mode, variant, heads):
@@ -75,7 +77,7 @@ def test_ragged_fp16(mode, variant, heads):
     assert_close(run(c, variant), oracle_fp16(c), what=f"mode {mode} {variant} {heads}")
 
 
-@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp_int8", "splitk_int8"])
 @pytest.mark.parametrize("heads", [(16, 8), (32, 1)])
 def test_ragged_int8(mode, variant, heads):
@@ -85,7 +87,7 @@ def test_ragged_int8(mode, variant, heads):
     assert_close(run(c, variant, int8=True), oracle_int8(c), what=f"mode {mode} {variant}")
 
 
-@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp", "splitk"])
 def test_capacity_sized_block_table(mode, variant):
     """A block table sized for a long maximum length with short sequences in it
@@ -109,11 +111,14 @@ def test_many_sequences(num_seqs, variant):
     assert_close(run(c, variant), oracle_fp16(c), what=f"{num_seqs} seqs")
     _mode(SCHED)
     assert_close(run(c, variant), oracle_fp16(c), what=f"{num_seqs} seqs, schedule forced")
+    _mode(STREAM)
+    assert_close(run(c, variant), oracle_fp16(c), what=f"{num_seqs} seqs, stream partition")
 
 
+@pytest.mark.parametrize("mode", [SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp", "splitk", "warp_int8", "splitk_int8"])
-def test_schedule_is_reproducible(variant):
-    _mode(SCHED)
+def test_schedule_is_reproducible(variant, mode):
+    _mode(mode)
     lens = ragged_lens(33, seed=21)
     int8 = variant.endswith("int8")
     c = (int8_case if int8 else fp16_case)(len(lens), lens, 16, 4, seed=15)
@@ -122,10 +127,12 @@ def test_schedule_is_reproducible(variant):
         assert np.array_equal(run(c, variant, int8=int8), a)
 
 
-def test_claim_counters_reset_between_shapes():
+@pytest.mark.parametrize("mode", [SCHED, STREAM])
+def test_claim_counters_reset_between_shapes(mode):
     """Different shapes and lengths back to back on one stream: every launch
-    must see zeroed claim and arrival counters."""
-    _mode(SCHED)
+    must see zeroed claim and arrival counters (and, under the stream
+    partition, scratch that the previous shape left)."""
+    _mode(mode)
     for i, (n, heads, hi) in enumerate([(9, (8, 2), 4000), (40, (16, 8), 600),
                                         (3, (32, 1), 9000), (64, (8, 2), 200)]):
         lens = ragged_lens(n, seed=40 + i, hi=hi)
@@ -134,11 +141,21 @@ def test_claim_counters_reset_between_shapes():
             assert_close(run(c, variant), oracle_fp16(c), what=f"shape {i} {variant}")
 
 
-@pytest.mark.parametrize("variant", ["warp", "splitk"])
-def test_schedule_zero_and_clamped_context(variant):
-    """No-check entry under the schedule: ctx <= 0 gives zeros, ctx beyond the
-    block table is clamped to it."""
-    _mode(SCHED)
+@pytest.mark.parametrize("mode", [SCHED, STREAM])
+@pytest.mark.parametrize("variant", ["warp", "splitk", "splitk_int8"])
+def test_schedule_zero_and_clamped_context(variant, mode):
+    """No-check entry under the schedule and the stream partition: ctx <= 0
+    gives zeros, ctx beyond the block table is clamped to it."""
+    _mode(mode)
+    if variant.endswith("int8"):
+        c = int8_case(4, np.array([40, 20, 33, 500], dtype=np.int32), 8, 2, seed=17)
+        lens = np.array([0, 20, 10_000, -3], dtype=np.int32)
+        got = run(c, variant, lens=lens, check=False, int8=True)
+        assert np.all(got[0] == 0) and np.all(got[3] == 0)
+        cap = c["block_table8"].shape[1] * c["block_size"]
+        c2 = dict(c, lens=np.array([1, 20, cap, 1], dtype=np.int32))
+        assert_close(got[1:3], oracle_int8(c2)[1:3], what="clamped")
+        return
     c = fp16_case(4, np.array([40, 20, 33, 500], dtype=np.int32), 8, 2, seed=17)
     lens = np.array([0, 20, 10_000, -3], dtype=np.int32)
     got = run(c, variant, lens=lens, check=False)
