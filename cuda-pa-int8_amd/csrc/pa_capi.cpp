@@ -106,6 +106,7 @@ struct Plan {
   int pmin_uniform = 0;   // lower bound the kernel uses when all lengths are equal
   bool nt_loads = false;  // non-temporal V-row loads
   bool k_nt = false;      // non-temporal K-row loads too
+  bool fused = false;     // splits merged in the same launch (last-arriving work-group)
 };
 
 Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_heads,
@@ -127,6 +128,15 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
              (long long)num_seqs * ((cap + 31) / 32) * num_heads < (1ll << 31);
   if (num_seqs > pa::kSchedMaxSeqs) p.sched = p.stream = false;
   if (p.stream) p.sched = false;
+  // Split merge: the single-launch kinds merge in the launch by definition;
+  // under the in-kernel schedule the split-K kinds do too (the last
+  // work-group of a unit merges its splits while the other work-groups still
+  // stream) instead of a separate reduce launch.  Same-box A/B on MI355X,
+  // split-K + reduce -> merged: MQA 32/1 of bench config 5 FP16 68.2 -> 60.5 us,
+  // INT8 49.5 -> 44.5 us; config 4 32k INT8 95.6 -> 90.6 us; config 2 29.7 ->
+  // 28.2 us; config 5 32/8 INT8 174.4 -> 169.4 us (FP16 279 -> 284 us, the one
+  // loss).  The grid and stream forms of split-K keep their reduce launch.
+  p.fused = is_fused(kind) || p.sched;
   // Head tile: up to 32 query heads (two MFMA column tiles) for head_dim <=
   // 128, except under the in-kernel schedule, which keeps 16.  (There, MQA
   // 32/1 of bench config 5 ran no faster with one 32-head work-group per row
@@ -345,7 +355,7 @@ pa_status_t decode_common(const pa::DecodeCall& c, void* counters, size_t counte
   l.head_dim = head_dim;
   l.waves = p.waves;
   l.int8_kv = !is_f16(kind);
-  l.fused = is_fused(kind);
+  l.fused = p.fused;
   l.nt_loads = p.nt_loads;
   l.k_nt = p.k_nt;
   l.stream = reinterpret_cast<hipStream_t>(stream);

@@ -1303,8 +1303,15 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
     // The next item is claimed once this item's first loads are out.
     uint32_t old = 0;
     auto claim = [&] {
-      if (claims && threadIdx.x == 0)
-        old = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (claims && threadIdx.x == 0) {
+        // The address is kept from looking uniform: the compiler's
+        // wave-aggregated form of a uniform-address atomic reads the answer
+        // at once, and that wait (the memory counter completes in order)
+        // would also wait for this item's first K/V rows.
+        int z = 0;
+        asm volatile("" : "+v"(z));
+        old = __hip_atomic_fetch_add(queue + z, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     };
     const int row = cls + 8 * (idx / per_row);
     const int sub = idx - (idx / per_row) * per_row;
