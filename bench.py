@@ -256,8 +256,62 @@ def gate_seqs(lens, n=6):
 
 # --------------------------------------------------------------------------- configs
 
+PLAN_FIELDS = ("partition_tokens", "splits", "waves", "head_tile", "distribution", "load_hints",
+               "merged_in_launch")
+
+
+def plan_detail(variant, case, partition=0):
+    """The plan the library runs `variant` under for this case
+    (pa_decode_plan_detail of the tuning header), as a dict."""
+    import ctypes
+
+    import pa_int8
+
+    kind = pa_int8.registry.KIND[variant]
+    q, bt = case["q"], case["bt"]
+    info = (ctypes.c_int32 * 7)()
+    st = pa_int8.capi().pa_decode_plan_detail(kind, q.shape[0], q.shape[1], q.shape[2],
+                                              case["kv_heads"], case["bs"], bt.shape[1], 0,
+                                              partition, info, 7)
+    if st != 0:
+        raise RuntimeError(f"pa_decode_plan_detail: status {st}")
+    return dict(zip(PLAN_FIELDS, list(info)))
+
+
+def probe_decode_stream(torch, case, variant, steps, warmup, replays=3):
+    """Time of the exact-address-stream probe (libpa_bench_probe.so): the
+    decode launch's own loads over the same caches, block table and plan, with
+    the attention math replaced by a checksum.  Grid-form plans only (the
+    single-launch kinds at up to 16 query heads per kv head, head_dim 128);
+    None otherwise."""
+    from pa_int8._loader import probe_capi
+
+    plan = plan_detail(variant, case)
+    q = case["q"]
+    if plan["distribution"] != 1 or plan["head_tile"] != case["heads"] // case["kv_heads"] \
+            or q.shape[2] != 128:
+        return None
+    lib = probe_capi()
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    int8 = variant.endswith("int8")
+    fns = []
+    for kc, vc, ks, vs in case["caches"]:
+        def fn(kc=kc, vc=vc, ks=ks, vs=vs):
+            st = lib.pa_probe_decode_stream(
+                1 if int8 else 0, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                ks.data_ptr() if int8 else None, vs.data_ptr() if int8 else None,
+                case["bt"].data_ptr(), case["ctx"].data_ptr(), q.shape[0], q.shape[1],
+                case["kv_heads"], case["bs"], kc.shape[0], case["bt"].shape[1], 0,
+                plan["partition_tokens"], plan["waves"], plan["load_hints"], sink.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"pa_probe_decode_stream: status {st}")
+        fns.append(fn)
+    return time_steps(torch, fns, steps, warmup, replays)
+
+
 def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0, outliers=False,
-                   replays=3, eager=False, partition=0, eager_only=False):
+                   replays=3, eager=False, partition=0, eager_only=False, probe=False):
     from pa_int8 import metrics
 
     int8 = variant.endswith("int8")
@@ -289,6 +343,16 @@ def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0,
                steps=steps, ok=checked["ok"], gate=checked)
     if eager:
         res["eager_us"] = round(time_eager(torch, fns, steps) * 1e3, 2)
+    if probe and not eager_only:
+        pms = probe_decode_stream(torch, case, variant, steps, warmup, replays)
+        if pms is not None:
+            res["address_stream_probe"] = dict(
+                us=round(pms * 1e3, 2), gbs=round(nbytes / (pms * 1e-3) / 1e9, 1),
+                decode_over_probe=round(ms / pms, 4),
+                what="the decode launch's own loads (same plan, caches and block table) with "
+                     "the attention math replaced by a checksum")
+            log(f"[bench] {name} {variant} address-stream probe: {res['address_stream_probe']['us']} "
+                f"us (decode / probe = {ms / pms:.3f})")
     del case, fns
     torch.cuda.empty_cache()
     log(f"[bench] {name} {variant}: {res['us']} us, {res['gbs']} GB/s "
@@ -521,9 +585,9 @@ def run_configs(torch, names, steps, warmup):
     if "cfg3" in names:
         lens = [8192] * 64
         r8 = run_decode_cfg(torch, "cfg3", lens, 12, 2, 128, "warp_int8", steps_for(40, steps),
-                            warmup)
+                            warmup, probe=True)
         r16 = run_decode_cfg(torch, "cfg3", lens, 12, 2, 128, "warp", steps_for(80, steps),
-                             warmup)
+                             warmup, probe=True)
         out["cfg3_qwen_int8"] = r8
         out["cfg3_qwen_fp16_same_shape"] = r16
         out["cfg3_int8_over_fp16_latency"] = round(r8["us"] / r16["us"], 3)
@@ -766,7 +830,7 @@ def main():
     # ---- headline: config 2, single-launch FP16
     lens = [4096] * 32
     head = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "warp", args.steps, args.warmup,
-                          replays=1, eager=True, eager_only=args.eager)
+                          replays=1, eager=True, eager_only=args.eager, probe=True)
     head_sk = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "splitk", args.steps, args.warmup)
     ms = head["us"] / 1e3
     nbytes = head["algo_bytes"]

@@ -33,6 +33,25 @@ pa_status_t pa_probe_read_chunks(const void* src, size_t bytes, const int32_t* o
 pa_status_t pa_probe_read_write(const void* src, size_t read_bytes, void* dst, int32_t grid,
                                 pa_stream_t stream);
 
+/* pa_probe_decode_stream issues exactly the loads of one grid decode launch
+ * (the single-launch kinds, head_dim 128, at most 16 query heads per kv head)
+ * and folds the loaded words into a checksum instead of computing attention:
+ * its time is the memory system's for the decode's address stream.  The
+ * arguments are those of the decode call, plus the plan it runs under
+ * (pa_decode_plan_detail of pa_mi355x_tuning.h): partition_tokens, waves (4
+ * or 8) and load_flags (bit 0: non-temporal V rows, bit 1: non-temporal K
+ * rows, FP16 only).  int8_kv selects the INT8 layout (k_scales / v_scales
+ * required). */
+pa_status_t pa_probe_decode_stream(int32_t int8_kv, const void* q, const void* k_cache,
+                                   const void* v_cache, const float* k_scales,
+                                   const float* v_scales, const int32_t* block_table,
+                                   const int32_t* context_lens, int32_t num_seqs,
+                                   int32_t num_heads, int32_t num_kv_heads, int32_t block_size,
+                                   int32_t num_blocks, int32_t max_blocks_per_seq,
+                                   int32_t max_context_len, int32_t partition_tokens,
+                                   int32_t waves, int32_t load_flags, uint32_t* sink,
+                                   pa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

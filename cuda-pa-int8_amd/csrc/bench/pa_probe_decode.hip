@@ -1,0 +1,248 @@
+// Exact-address-stream probe of the grid decode (the single-launch kinds):
+// the same launch (work-groups, waves, work items and their XCD grouping),
+// the same prologue loads (context length, the split's block ids staged in
+// LDS, the query rows) and the same K/V rows and INT8 scales, loaded by the
+// same DecodeWave routines with the same cache hints in the same software
+// pipeline as decode_split -- but with every loaded word folded into a
+// checksum instead of the QK product, softmax, PV product and merges.  Its
+// time is the memory system's for exactly the decode's address stream: the
+// ceiling the decode kernel is measured against.  head_dim 128, up to 16
+// query heads per kv head (one column tile), as benchmark configs 2 and 3.
+// Measurement helper of libpa_bench_probe.so (declared in pa_probe.h).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "pa_decode_kernels.hpp"
+#include "pa_probe.h"
+
+namespace pa {
+namespace {
+
+constexpr int kProbeD = 128;
+
+__device__ __forceinline__ uint32_t fold4(uint4 v) { return v.x ^ v.y ^ v.z ^ v.w; }
+__device__ __forceinline__ uint32_t fold2(uint2 v) { return v.x ^ v.y; }
+__device__ __forceinline__ uint32_t foldf(float f) { return __float_as_uint(f); }
+
+template <int NW, bool I8, bool NTL, bool KNT>
+__global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
+probe_decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, DecodeShape sh,
+                    const half_t* __restrict__ q, const uint8_t* __restrict__ kc,
+                    const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
+                    const float* __restrict__ vsc, uint32_t* __restrict__ sink) {
+  constexpr int D = kProbeD;
+  using Wave = DecodeWave<D, 1, I8>;
+  using Blocks = typename Wave::Blocks;
+  constexpr int PAIRS = Wave::PAIRS;
+  constexpr int IT = Wave::IT;
+  constexpr int KC = Wave::KC;
+  constexpr int NT = Wave::NT;
+  constexpr bool W8 = Wave::W8;
+  constexpr int kStage = split_blocks_max<D, NW>();
+  __shared__ int blk[kStage];
+
+  GridItem it;
+  if (!grid_item(sh, blockIdx.x, it)) return;
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int bsl = sh.bs_log2;
+  const int t_begin = it.split * sh.partition;
+  const int head0 = it.kvh * sh.group + it.chunk * sh.head_tile;
+  const CacheView cv{kc, vc, ksc, vsc, sh.num_kv_heads, sh.block_size, sh.num_blocks};
+  Wave dw;
+  dw.init(lane);
+
+  // prologue: as decode_kernel / decode_split
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const int ctx_lane = ctxl[it.seq + zero];
+  const int* btrow = bt + (size_t)it.seq * sh.max_blocks;
+  const int b_first = t_begin >> bsl;
+  constexpr int kStageRegs = (kStage + NW * kWave - 1) / (NW * kWave);
+  int nstage = min(((t_begin + sh.partition - 1) >> bsl) - b_first + 1, sh.max_blocks - b_first);
+  nstage = nstage < 0 ? 0 : min(nstage, kStage);
+  int staged[kStageRegs];
+#pragma unroll
+  for (int k = 0; k < kStageRegs; ++k) {
+    const int i = tid + k * NW * kWave;
+    staged[k] = i < nstage ? btrow[b_first + i] : 0;
+  }
+  dw.load_q(q, (size_t)it.seq * sh.num_heads + head0, sh.head_tile);
+  uint32_t acc = 0;
+#pragma unroll
+  for (int kk = 0; kk < KC; ++kk) acc ^= fold4(__builtin_bit_cast(uint4, dw.qreg[0][kk]));
+  const int ctx = grid_ctx(sh, __builtin_amdgcn_readfirstlane(ctx_lane));
+  const int ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
+  if (it.split >= ns) return;
+  const int t_end = min(ctx, t_begin + sh.partition);
+  const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
+  const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1, nstage) : 0;
+#pragma unroll
+  for (int k = 0; k < kStageRegs; ++k) {
+    const int i = tid + k * NW * kWave;
+    if (i < nstage) blk[i] = staged[k];
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+
+  auto load_blocks = [&](int it_, Blocks& b) {
+    int kt[PAIRS], vt[PAIRS];
+    dw.block_tokens(t_begin + it_ * IT, t_end, t_begin, kt, vt);
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      const int ki = (kt[p] >> bsl) - b_first;
+      const int vi = (vt[p] >> bsl) - b_first;
+      b.kb[p] = blk[ki < nblk ? ki : 0];
+      b.vb[p] = blk[vi < nblk ? vi : 0];
+    }
+  };
+  auto fold_k = [&] {
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p)
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        if constexpr (W8) acc ^= fold4(dw.kw[p][kk]);
+        else if constexpr (I8) acc ^= fold2(dw.kx[p][kk]) ^ fold2(dw.ky[p][kk]);
+        else acc ^= fold4(dw.kx[p][kk]) ^ fold4(dw.ky[p][kk]);
+      }
+  };
+  auto fold_v = [&](const typename Wave::W8Buf& sc) {
+    if constexpr (W8) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc ^= fold4(dw.vw[t]);
+      acc ^= foldf(sc.ks4.x) ^ foldf(sc.ks4.y) ^ foldf(sc.ks4.z) ^ foldf(sc.ks4.w);
+      acc ^= foldf(sc.vs4.x) ^ foldf(sc.vs4.y) ^ foldf(sc.vs4.z) ^ foldf(sc.vs4.w);
+    } else {
+#pragma unroll
+      for (int p = 0; p < PAIRS; ++p) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if constexpr (I8) acc ^= fold2(dw.vr[p][t]);
+          else acc ^= fold4(dw.vr[p][t]);
+        }
+        if constexpr (I8) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc ^= foldf(dw.ksv[p][j]) ^ foldf(dw.vsv[p][j]);
+        }
+      }
+    }
+  };
+
+  // the rotated pipeline of decode_split, with folds in place of the math
+  if (w < n_it) {
+    {
+      Blocks b0;
+      load_blocks(w, b0);
+      const int tok0 = t_begin + w * IT;
+      if constexpr (W8) dw.issue_scales(cv, it.kvh, tok0, t_end, t_begin, b0, dw.wa);
+      dw.template issue_k<KNT>(cv, it.kvh, tok0, t_end, t_begin, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      dw.template issue_v<NTL>(cv, it.kvh, tok0, t_end, t_begin, b0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    fold_k();
+    __builtin_amdgcn_sched_barrier(0);
+    int nxt = w + NW;
+    while (nxt < n_it) {
+      const typename Wave::W8Buf cur = dw.wa;
+      Blocks bn;
+      load_blocks(nxt, bn);
+      const int tok0 = t_begin + nxt * IT;
+      if constexpr (W8) dw.issue_scales(cv, it.kvh, tok0, t_end, t_begin, bn, dw.wa);
+      dw.template issue_k<KNT>(cv, it.kvh, tok0, t_end, t_begin, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      fold_v(cur);
+      __builtin_amdgcn_sched_barrier(0);
+      dw.template issue_v<NTL>(cv, it.kvh, tok0, t_end, t_begin, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      fold_k();
+      __builtin_amdgcn_sched_barrier(0);
+      nxt += NW;
+    }
+    fold_v(dw.wa);
+  }
+  // The checksum reaches memory only on a practically impossible value, so no
+  // load can be dropped and nothing else is written.
+  if (acc == 0x9E3779B9u) sink[blockIdx.x & 1023] = acc;
+}
+
+template <int NW, bool I8>
+hipError_t launch_probe(dim3 grid, bool nt_v, bool nt_k, hipStream_t st, const int* bt,
+                        const int* ctxl, const DecodeShape& sh, const half_t* q, const uint8_t* kc,
+                        const uint8_t* vc, const float* ksc, const float* vsc, uint32_t* sink) {
+  const int nth = NW * kWave;
+  if (nt_v && nt_k && !I8)
+    probe_decode_kernel<NW, I8, true, true><<<grid, nth, 0, st>>>(bt, ctxl, sh, q, kc, vc, ksc,
+                                                                  vsc, sink);
+  else if (nt_v)
+    probe_decode_kernel<NW, I8, true, false><<<grid, nth, 0, st>>>(bt, ctxl, sh, q, kc, vc, ksc,
+                                                                   vsc, sink);
+  else
+    probe_decode_kernel<NW, I8, false, false><<<grid, nth, 0, st>>>(bt, ctxl, sh, q, kc, vc, ksc,
+                                                                    vsc, sink);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace pa
+
+extern "C" pa_status_t pa_probe_decode_stream(
+    int32_t int8_kv, const void* q, const void* k_cache, const void* v_cache,
+    const float* k_scales, const float* v_scales, const int32_t* block_table,
+    const int32_t* context_lens, int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+    int32_t block_size, int32_t num_blocks, int32_t max_blocks_per_seq, int32_t max_context_len,
+    int32_t partition_tokens, int32_t waves, int32_t load_flags, uint32_t* sink,
+    pa_stream_t stream) {
+  if (!q || !k_cache || !v_cache || !block_table || !context_lens || !sink ||
+      (int8_kv && (!k_scales || !v_scales)))
+    return PA_ERR_NULL_POINTER;
+  if (num_seqs < 1 || num_kv_heads < 1 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > pa::kMaxGroupTile || block_size < 16 ||
+      (block_size & (block_size - 1)) != 0 || num_blocks < 1 || max_blocks_per_seq < 1 ||
+      partition_tokens < pa::kIterTokens || partition_tokens % pa::kIterTokens != 0 ||
+      partition_tokens > pa::max_partition_per_4_waves(pa::kProbeD) * waves / 4 ||
+      (waves != 4 && waves != 8))
+    return PA_ERR_BAD_SHAPE;
+  pa::DecodeShape sh{};
+  sh.num_seqs = num_seqs;
+  sh.num_heads = num_heads;
+  sh.num_kv_heads = num_kv_heads;
+  sh.group = num_heads / num_kv_heads;
+  sh.head_tile = sh.group;
+  sh.nchunk = 1;
+  sh.block_size = block_size;
+  int l2 = 0;
+  while ((1 << l2) < block_size) ++l2;
+  sh.bs_log2 = l2;
+  sh.num_blocks = num_blocks;
+  sh.max_blocks = max_blocks_per_seq;
+  sh.partition = partition_tokens;
+  const long long cap = (long long)max_blocks_per_seq * block_size;
+  const long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
+  sh.nsplit = (int)((std::max(1ll, ctx) + partition_tokens - 1) / partition_tokens);
+  sh.num_items = num_seqs * sh.nsplit;
+  // the grid of launch_decode_tiles
+  const int grid = sh.num_items >= 8 ? (sh.num_items + 7) / 8 * 8 * num_kv_heads
+                                     : (sh.num_items * num_kv_heads + 7) / 8 * 8;
+  const bool nt_v = (load_flags & 1) != 0, nt_k = (load_flags & 2) != 0;
+  const auto st = reinterpret_cast<hipStream_t>(stream);
+  const auto* qh = static_cast<const pa::half_t*>(q);
+  const auto* kc = static_cast<const uint8_t*>(k_cache);
+  const auto* vc = static_cast<const uint8_t*>(v_cache);
+  hipError_t e;
+  if (int8_kv)
+    e = waves == 8 ? pa::launch_probe<8, true>(grid, nt_v, nt_k, st, block_table, context_lens,
+                                                 sh, qh, kc, vc, k_scales, v_scales, sink)
+                   : pa::launch_probe<4, true>(grid, nt_v, nt_k, st, block_table, context_lens,
+                                                 sh, qh, kc, vc, k_scales, v_scales, sink);
+  else
+    e = waves == 8 ? pa::launch_probe<8, false>(grid, nt_v, nt_k, st, block_table, context_lens,
+                                                  sh, qh, kc, vc, k_scales, v_scales, sink)
+                   : pa::launch_probe<4, false>(grid, nt_v, nt_k, st, block_table, context_lens,
+                                                  sh, qh, kc, vc, k_scales, v_scales, sink);
+  return e == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
+}

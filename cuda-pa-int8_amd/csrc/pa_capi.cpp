@@ -465,6 +465,23 @@ pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_
   return PA_OK;
 }
 
+pa_status_t pa_decode_plan_detail(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                                  int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                                  int32_t max_blocks_per_seq, int32_t max_context_len,
+                                  int32_t partition_tokens, int32_t* info, int32_t n) {
+  if (!info && n > 0) return PA_ERR_NULL_POINTER;
+  pa_status_t st = pa_validate_decode(kind, num_seqs, num_heads, head_dim, num_kv_heads, 1,
+                                      block_size, 8, std::max(1, max_blocks_per_seq));
+  if (st != PA_OK) return st;
+  const Plan p = make_plan(kind, num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+                           std::max(1, max_blocks_per_seq), max_context_len, partition_tokens);
+  const int32_t v[7] = {p.partition, p.nsplit, p.waves, p.head_tile,
+                        p.stream ? 3 : (p.sched ? 2 : 1),
+                        (p.nt_loads ? 1 : 0) | (p.k_nt ? 2 : 0), p.fused ? 1 : 0};
+  for (int i = 0; i < n && i < 7; ++i) info[i] = v[i];
+  return PA_OK;
+}
+
 size_t pa_decode_workspace_bytes(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
                                  int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
                                  int32_t max_blocks_per_seq, int32_t max_context_len,

@@ -148,60 +148,76 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 // same bits the compiler uses for agent-scope atomic loads and stores.
 constexpr int kPolicyDevice = 16;
 
-// Merge the `ns` partials of one unit (gt heads) and write its fp16 output
-// rows.  The partial of split sp sits in slot slot_of(sp): acc[gt][D]
-// (relative to its max) and (m, l) per head.  Thread i owns (head, 4-dim
-// chunk) items i, i + THREADS, ... and merges them without LDS or barriers:
-// the (m, l) pairs and accumulators of 8 splits at a time are loaded in one
-// batch and folded into a running (max, sum, acc).
+// Folds the partials of splits [0, ns) of one unit, in split order, into the
+// running (max, sum, accumulator) (M, L, A) of item (head h, dims 4c .. 4c +
+// 3); M = -inf: nothing folded yet.  The partial of split sp sits in slot
+// slot_of(sp): acc[gt][D] (relative to its max) and (m, l) per head.  The
+// (m, l) pairs and accumulators of 8 splits at a time are loaded in one batch.
 // COHERENT: device-coherent loads (partials written in this launch).
+template <int D, bool COHERENT, typename SlotOf>
+__device__ __forceinline__ void fold_splits(const float* __restrict__ pacc,
+                                            const float* __restrict__ pml, SlotOf slot_of, int gt,
+                                            int h, int c, int ns, float& M, float& L, f4_t& A) {
+  constexpr int SB = 8;
+  constexpr int POL = COHERENT ? kPolicyDevice : 0;
+  const uint32_t acc_bytes = (uint32_t)(gt * D * 4), ml_bytes = (uint32_t)(gt * 8);
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    f4_t v[SB];
+    f2_t ml[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      // Past the last split the last one is re-read (and weighted 0), so
+      // every load of the batch is unconditional.
+      const size_t slot = slot_of(min(s0 + u, ns - 1));
+      const auto ra = buf_rsrc(pacc + slot * gt * D, acc_bytes);
+      const auto rm = buf_rsrc(pml + slot * gt * 2, ml_bytes);
+      v[u] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * c) * 4, 0, POL));
+      ml[u] = __builtin_bit_cast(f2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, 0, POL));
+    }
+    float mb = M;
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (s0 + u < ns) mb = fmaxf(mb, ml[u].x);
+    const float fo = M == kNegInf ? 0.f : exp2f_fast(M - mb);
+    A *= fo;
+    L *= fo;
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const float f = (s0 + u < ns && ml[u].x != kNegInf) ? exp2f_fast(ml[u].x - mb) : 0.f;
+      A += v[u] * f;
+      L += ml[u].y * f;
+    }
+    M = mb;
+  }
+}
+
+// The normalised fp16 output of item (head h, dims 4c .. 4c + 3).
+template <int D>
+__device__ __forceinline__ void write_out_item(half_t* __restrict__ out, size_t out_base, int h,
+                                               int c, float L, f4_t A) {
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const uint2 pk = make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
+  *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
+}
+
+// Merge the `ns` partials of one unit (gt heads) and write its fp16 output
+// rows.  Thread i owns (head, 4-dim chunk) items i, i + THREADS, ... and merges
+// them without LDS or barriers.
 template <int D, int THREADS, bool COHERENT, typename SlotOf>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
                                              const float* __restrict__ pml,
                                              half_t* __restrict__ out, SlotOf slot_of, int gt,
                                              size_t out_base, int ns) {
   constexpr int CH = D / 4;
-  constexpr int SB = 8;
-  constexpr int POL = COHERENT ? kPolicyDevice : 0;
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));   // nothing lane-dependent is hoisted out of a caller's loop
   const int nitems = gt * CH;
-  const uint32_t acc_bytes = (uint32_t)(gt * D * 4), ml_bytes = (uint32_t)(gt * 8);
   for (int i = tid; i < nitems; i += THREADS) {
     const int h = i / CH, c = i - h * CH;
     float M = kNegInf, L = 0.f;
     f4_t A = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < ns; s0 += SB) {
-      f4_t v[SB];
-      f2_t ml[SB];
-#pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        // Past the last split the last one is re-read (and weighted 0), so
-        // every load of the batch is unconditional.
-        const size_t slot = slot_of(min(s0 + u, ns - 1));
-        const auto ra = buf_rsrc(pacc + slot * gt * D, acc_bytes);
-        const auto rm = buf_rsrc(pml + slot * gt * 2, ml_bytes);
-        v[u] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * c) * 4, 0, POL));
-        ml[u] = __builtin_bit_cast(f2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, 0, POL));
-      }
-      float mb = M;
-#pragma unroll
-      for (int u = 0; u < SB; ++u)
-        if (s0 + u < ns) mb = fmaxf(mb, ml[u].x);
-      const float fo = M == kNegInf ? 0.f : exp2f_fast(M - mb);
-      A *= fo;
-      L *= fo;
-#pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const float f = (s0 + u < ns && ml[u].x != kNegInf) ? exp2f_fast(ml[u].x - mb) : 0.f;
-        A += v[u] * f;
-        L += ml[u].y * f;
-      }
-      M = mb;
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const uint2 pk = make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
-    *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
+    fold_splits<D, COHERENT>(pacc, pml, slot_of, gt, h, c, ns, M, L, A);
+    write_out_item<D>(out, out_base, h, c, L, A);
   }
 }
 
@@ -750,10 +766,46 @@ struct DecodeWave {
   }
 };
 
+// The NW wave states of item (head hh of a column tile, dims 4c .. 4c + 3) in
+// LDS, merged: accumulator relative to the max, the max and the sum.
+template <int D, int NW, typename Smem>
+__device__ __forceinline__ void wave_state_item(const Smem& sm, int hh, int c, f4_t& A, float& M,
+                                                float& L) {
+  float mw[NW];
+  M = kNegInf;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    mw[v] = sm.m[v][hh];
+    M = fmaxf(M, mw[v]);
+  }
+  A = (f4_t){0.f, 0.f, 0.f, 0.f};
+  L = 0.f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    const float f = mw[v] == kNegInf ? 0.f : exp2f_fast(mw[v] - M);
+    L += sm.l[v][hh] * f;
+    A += *reinterpret_cast<const f4_t*>(&sm.a[v][hh][4 * c]) * f;
+  }
+}
+
+// One item's partial (acc, then (max, sum) per head) through the buffer
+// resources racc / rml (device-coherent, write-through stores when COHERENT).
+template <int D, bool COHERENT>
+__device__ __forceinline__ void store_partial_item(__amdgpu_buffer_rsrc_t racc,
+                                                   __amdgpu_buffer_rsrc_t rml, int h, int c,
+                                                   f4_t A, float M, float L) {
+  constexpr int POL = COHERENT ? kPolicyDevice : 0;
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc, (h * D + 4 * c) * 4, 0,
+                                         POL);
+  if (c == 0) {
+    const f2_t ml = {M, L};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml), rml, h * 8, 0, POL);
+  }
+}
+
 // The NW wave states of column tile ct in LDS, merged per (head, 4-dim
 // chunk) item by the work-group's threads: the normalised fp16 output when
-// `final_out`, else a partial (acc, then (max, sum) per head) through the
-// buffer resources racc / rml (device-coherent stores when COHERENT).
+// `final_out`, else a partial.
 template <int D, int NW, bool COHERENT, typename Smem>
 __device__ __forceinline__ void merge_wave_states(const Smem& sm, int ct, int nh,
                                                   int tid, bool final_out,
@@ -764,36 +816,11 @@ __device__ __forceinline__ void merge_wave_states(const Smem& sm, int ct, int nh
   for (int i = tid; i < nh * CH; i += NW * kWave) {
     const int hh = i / CH, c = i - hh * CH;
     const int h = 16 * ct + hh;             // head within the unit's tile
-    float mw[NW], M = kNegInf;
-#pragma unroll
-    for (int v = 0; v < NW; ++v) {
-      mw[v] = sm.m[v][hh];
-      M = fmaxf(M, mw[v]);
-    }
-    f4_t A = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
-#pragma unroll
-    for (int v = 0; v < NW; ++v) {
-      const float f = mw[v] == kNegInf ? 0.f : exp2f_fast(mw[v] - M);
-      L += sm.l[v][hh] * f;
-      A += *reinterpret_cast<const f4_t*>(&sm.a[v][hh][4 * c]) * f;
-    }
-    if (final_out) {
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      const uint2 pk =
-          make_uint2(pack_h2(A[0] * inv, A[1] * inv), pack_h2(A[2] * inv, A[3] * inv));
-      *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
-    } else {
-      // COHERENT: device-coherent (write-through) stores, visible to every XCD
-      // once this thread's stores are acknowledged.
-      constexpr int POL = COHERENT ? kPolicyDevice : 0;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc,
-                                             (h * D + 4 * c) * 4, 0, POL);
-      if (c == 0) {
-        const f2_t ml = {M, L};
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml), rml, h * 8, 0, POL);
-      }
-    }
+    f4_t A;
+    float M, L;
+    wave_state_item<D, NW>(sm, hh, c, A, M, L);
+    if (final_out) write_out_item<D>(out, out_base, h, c, L, A);
+    else store_partial_item<D, COHERENT>(racc, rml, h, c, A, M, L);
   }
 }
 
@@ -940,10 +967,10 @@ __device__ __forceinline__ void decode_split(
   // goes to LDS; then the work-group's threads merge them and write the
   // output when the unit has one split, else this split's partial.
   const size_t out_base = ((size_t)seq * sh.num_heads + head0) * D;
-  const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
   const size_t slot = wk.slot0 + (size_t)split * wk.stride;
   const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
   const auto rml = buf_rsrc(pml + slot * gt * 2, (uint32_t)(gt * 8));
+  const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int nh = min(16, gt - 16 * ct);   // query heads of this tile
@@ -956,6 +983,9 @@ __device__ __forceinline__ void decode_split(
     if (ns_eff > 1) {
       // Wait until this thread's partial stores are acknowledged, then count
       // the arrival; the last work-group of the unit merges every split.
+      // (An arrival counted before the stores, so that the last work-group
+      // could keep its own partial in registers, measured slower: the last
+      // one then waits for the others' stores, by device-scope polling.)
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       __builtin_amdgcn_s_waitcnt(0);
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -1000,6 +1030,50 @@ __device__ __forceinline__ void decode_split(
   sh.num_seqs = sh_num_seqs;                                                              \
   sh.num_blocks = sh_num_blocks
 
+// Work item of work-group wg in the grid form (XCD-aware); false past the
+// plan's items.  With at least 8 (sequence, split) items, an item's kv heads
+// and head chunks get work-group indices 8 apart, so they share blockIdx % 8
+// (their XCD under round-robin dispatch), run at about the same time and meet
+// in that XCD's L2: they read the same block-table lines, the head chunks of
+// a kv head the same K/V tiles, and with INT8 all kv heads of a block the same
+// scale lines (the block's scales are adjacent).  With fewer items that would
+// leave XCDs idle, so the kv heads are spread over the XCDs and only the head
+// chunks are grouped.
+struct GridItem {
+  int seq, kvh, chunk, split;
+};
+
+__device__ __forceinline__ bool grid_item(const DecodeShape& sh, int wg, GridItem& it) {
+  const bool by_item = sh.num_items >= 8;
+  const int per = by_item ? sh.num_kv_heads * sh.nchunk : sh.nchunk;
+  const int grp = wg / (8 * per);
+  const int rem = wg - grp * 8 * per;
+  const int sub = rem >> 3;
+  const int idx = grp * 8 + (rem & 7);
+  if (by_item) {
+    if (idx >= sh.num_items) return false;
+    it.split = idx % sh.nsplit;
+    it.seq = idx / sh.nsplit;
+    it.kvh = sub / sh.nchunk;
+    it.chunk = sub - it.kvh * sh.nchunk;
+  } else {
+    if (idx >= sh.num_items * sh.num_kv_heads) return false;
+    it.split = idx % sh.nsplit;
+    const int sk = idx / sh.nsplit;
+    it.kvh = sk % sh.num_kv_heads;
+    it.seq = sk / sh.num_kv_heads;
+    it.chunk = sub;
+  }
+  return true;
+}
+
+// A context length clamped to what the block table holds and to what the
+// grid's splits cover (no work-group reads past the table or the partials).
+__device__ __forceinline__ int grid_ctx(const DecodeShape& sh, int ctx_raw) {
+  const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
+  return ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
+}
+
 // Grid form: one work-group per (unit, split) slot of the host's plan.
 template <int D, int NW, int CT, bool I8, bool FUSED, bool NTL, bool KNT>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1012,51 +1086,21 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
   static_assert(sizeof(DecodeSmem<D, NW>) * (kWavesPerCU / NW) <= kLdsPerCU, "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
 
-  // ---- work item (XCD-aware).  With at least 8 (sequence, split) items, an
-  // item's kv heads and head chunks get work-group indices 8 apart, so they
-  // share blockIdx % 8 (their XCD under round-robin dispatch), run at about
-  // the same time and meet in that XCD's L2: they read the same block-table
-  // lines, the head chunks of a kv head the same K/V tiles, and with INT8 all
-  // kv heads of a block the same scale lines (the block's scales are
-  // adjacent).  With fewer items that would leave XCDs idle, so the kv heads
-  // are spread over the XCDs and only the head chunks are grouped.
-  const int wg = blockIdx.x;
-  const bool by_item = sh.num_items >= 8;
-  const int per = by_item ? sh.num_kv_heads * sh.nchunk : sh.nchunk;
-  const int grp = wg / (8 * per);
-  const int rem = wg - grp * 8 * per;
-  const int sub = rem >> 3;
-  const int idx = grp * 8 + (rem & 7);
-  int seq, kvh, chunk, split;
-  if (by_item) {
-    if (idx >= sh.num_items) return;
-    split = idx % sh.nsplit;
-    seq = idx / sh.nsplit;
-    kvh = sub / sh.nchunk;
-    chunk = sub - kvh * sh.nchunk;
-  } else {
-    if (idx >= sh.num_items * sh.num_kv_heads) return;
-    split = idx % sh.nsplit;
-    const int sk = idx / sh.nsplit;
-    kvh = sk % sh.num_kv_heads;
-    seq = sk / sh.num_kv_heads;
-    chunk = sub;
-  }
+  GridItem it;
+  if (!grid_item(sh, blockIdx.x, it)) return;
+  const int seq = it.seq, kvh = it.kvh, chunk = it.chunk, split = it.split;
 
-  // Contexts are clamped to what the block table holds and to what the grid's
-  // splits cover, so no work-group reads past the table or the partials.
-  // The length is used only after the split's block-id loads are issued.  It
-  // is read with a vector load at the top: a scalar load would be scheduled
-  // next to its first use, after the argument fetches of the query pointer.
+  // The context length is used only after the split's block-id loads are
+  // issued.  It is read with a vector load at the top: a scalar load would be
+  // scheduled next to its first use, after the argument fetches of the query
+  // pointer.
   int zero = 0;
   asm volatile("" : "+v"(zero));
   const int ctx_lane = ctxl[seq + zero];
   const int unit = (seq * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
   const SplitWork wk{seq, kvh, chunk, split, 0, sh.partition, 0, (size_t)unit * sh.nsplit, 1};
   auto resolve = [&](int& ctx, int& ns) {
-    const int ctx_raw = __builtin_amdgcn_readfirstlane(ctx_lane);
-    const int cap = min(sh.max_blocks * sh.block_size, sh.nsplit * sh.partition);
-    ctx = ctx_raw < 0 ? 0 : (ctx_raw > cap ? cap : ctx_raw);
+    ctx = grid_ctx(sh, __builtin_amdgcn_readfirstlane(ctx_lane));
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
     return split < ns;
   };

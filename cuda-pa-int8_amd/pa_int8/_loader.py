@@ -90,6 +90,8 @@ PROTOTYPES = {
     "pa_decode_set_schedule": (ctypes.c_int, [_i32]),
     "pa_decode_set_load_policy": (ctypes.c_int, [_i32]),
     "pa_decode_set_max_head_tile": (ctypes.c_int, [_i32]),
+    "pa_decode_plan_detail": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32, _i32,
+                                             _i32, _i32, _p, _i32]),
     "pa_paged_decode_attn_warp": (ctypes.c_int, _DECODE_F16_ARGS),
     "pa_paged_decode_attn_splitk": (ctypes.c_int, _DECODE_F16_ARGS),
     "pa_paged_decode_attn_warp_int8": (ctypes.c_int, _DECODE_I8_ARGS),
@@ -110,6 +112,8 @@ PROBE_PROTOTYPES = {
     "pa_probe_read_contiguous": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
     "pa_probe_read_chunks": (ctypes.c_int, [_p, _sz, _p, _i32, _i32, _p, _i32, _p]),
     "pa_probe_read_write": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
+    "pa_probe_decode_stream": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
+                                              _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
 }
 
 

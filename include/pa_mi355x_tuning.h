@@ -46,6 +46,17 @@ pa_status_t pa_decode_set_max_head_tile(int32_t heads);
  * 1 = plain; 2 = non-temporal. */
 pa_status_t pa_decode_set_load_policy(int32_t mode);
 
+/* The plan this thread's calls would run under for these arguments (the
+ * settings above included).  info receives up to n (<= 7) entries: [0] tokens
+ * per split, [1] splits, [2] waves per work-group, [3] query heads per
+ * work-group, [4] work distribution (1 grid, 2 in-kernel schedule, 3 stream
+ * partition), [5] load hints (bit 0: non-temporal V rows, bit 1: non-temporal
+ * K rows), [6] 1 when the splits are merged in the decode launch. */
+pa_status_t pa_decode_plan_detail(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
+                                  int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
+                                  int32_t max_blocks_per_seq, int32_t max_context_len,
+                                  int32_t partition_tokens, int32_t* info, int32_t n);
+
 #ifdef __cplusplus
 }
 #endif
