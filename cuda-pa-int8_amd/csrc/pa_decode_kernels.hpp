@@ -1116,8 +1116,10 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
 // about one item per resident work-group when all lengths are equal (the
 // grid plan's shape), about kSchedItemsPerGroup items per work-group
 // otherwise.  A row is one split of one sequence; rows that hold a full
-// partition come first, the shorter last rows of each sequence after them
-// (largest items first).  An item is (row, kv head, head chunk).  Items are
+// partition come first, the shorter last rows of the sequences after them,
+// longest first (in kShortBuckets bands of P / kShortBuckets tokens), so that
+// the items claimed last are the shortest and the launch does not wait on a
+// long one started late.  An item is (row, kv head, head chunk).  Items are
 // dealt to 8 claim classes by row, row % 8, with the kv heads and chunks of a
 // row next to each other; work-group b serves class b % 8 (its XCD under the
 // usual round-robin dispatch), starts with item b / 8 of its class
@@ -1136,10 +1138,14 @@ struct SchedArgs {
   int pmin_uniform;   // lower bound when all lengths are equal (one item per work-group)
 };
 
+constexpr int kShortBuckets = 4;   // (their counts pack into one 64-bit word)
+
 struct SchedSmem {
-  int full_pre[kSchedMaxSeqs + 1];   // exclusive prefix of full rows per sequence
-  int part_pre[kSchedMaxSeqs + 1];   // exclusive prefix of short last rows
-  uint16_t rem[kSchedMaxSeqs];       // context length % P (P <= 8192)
+  int full_pre[kSchedMaxSeqs + 1];        // exclusive prefix of full rows per sequence
+  uint16_t part_pre[kSchedMaxSeqs + 1];   // exclusive prefix of short last rows (<= S)
+  uint16_t rem[kSchedMaxSeqs];            // context length % P (P <= 8192)
+  uint16_t short_seq[kSchedMaxSeqs];      // sequence of short row j (longest first)
+  uint64_t band_scan[16];                 // per-wave totals of the band counts
   uint32_t red[3][16];               // per-wave sum (in 1024-token units), min, max
   int scan_f[16], scan_p[16];
   int next_item;
@@ -1161,6 +1167,17 @@ __device__ __forceinline__ uint32_t wave_reduce_u(uint32_t v, Op op) {
 struct OpAddU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
 struct OpMinU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
 struct OpMaxU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+
+// Inclusive prefix sum over the wave of 64-bit values.
+__device__ __forceinline__ uint64_t wave_scan_u64(uint64_t v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint64_t u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
 
 // Inclusive prefix sum over the wave.
 __device__ __forceinline__ int wave_scan_i(int v) {
@@ -1285,20 +1302,64 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
       sc.partition = P * 2 < sa.pmax ? P * 2 : sa.pmax;
       continue;
     }
+    // Short rows in bands of P / kShortBuckets tokens, longest band first, in
+    // sequence order inside a band.  Every work-group must derive the same
+    // order (the items are claimed from shared counters), so a row's place in
+    // its band is the number of earlier sequences in that band: one scan of
+    // the band counts, packed 16 bits per band (S <= 1024) into one word.
+    int band[E];
+    uint64_t cnt = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = tid * E + e;
+      const int r = c[e] % P;
+      band[e] = -1;
       if (i < S) {
         ss.full_pre[i] = fo;
-        ss.part_pre[i] = po;
-        ss.rem[i] = (uint16_t)(c[e] % P);
+        ss.part_pre[i] = (uint16_t)po;
+        ss.rem[i] = (uint16_t)r;
         fo += c[e] / P;
-        po += (c[e] % P != 0 || c[e] == 0) ? 1 : 0;
+        if (r != 0 || c[e] == 0) {
+          po += 1;
+          band[e] = (kShortBuckets - 1) - (int)((long long)r * kShortBuckets / P);
+          cnt += 1ull << (16 * band[e]);
+        }
       }
     }
     if (tid == 0) {
       ss.full_pre[S] = tf;
-      ss.part_pre[S] = tp;
+      ss.part_pre[S] = (uint16_t)tp;
+    }
+    const uint64_t incl = wave_scan_u64(cnt);
+    if (lane == kWave - 1) ss.band_scan[w] = incl;
+    __syncthreads();
+    uint64_t before = 0, total = 0;
+#pragma unroll
+    for (int v = 0; v < NWV; ++v) {
+      const uint64_t t = ss.band_scan[v];
+      if (v < w) before += t;
+      total += t;
+    }
+    // the bands' bases (exclusive prefix of their totals)
+    int bbase[kShortBuckets];
+    int acc_b = 0;
+#pragma unroll
+    for (int b = 0; b < kShortBuckets; ++b) {
+      bbase[b] = acc_b;
+      acc_b += (int)((total >> (16 * b)) & 0xFFFFu);
+    }
+    // this thread's first place in each band
+    uint64_t at = before + incl - cnt;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = tid * E + e;
+#pragma unroll
+      for (int b = 0; b < kShortBuckets; ++b) {
+        if (band[e] == b) {
+          ss.short_seq[bbase[b] + (int)((at >> (16 * b)) & 0xFFFFu)] = (uint16_t)i;
+          at += 1ull << (16 * b);
+        }
+      }
     }
     sc.n_full = tf;
     sc.n_rows = tf + tp;
@@ -1366,7 +1427,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
       seq = prefix_search(ss.full_pre, S, row);
       split = row - ss.full_pre[seq];
     } else {
-      seq = prefix_search(ss.part_pre, S, row - n_full);
+      seq = ss.short_seq[row - n_full];
       split = ss.full_pre[seq + 1] - ss.full_pre[seq];
     }
     seq = __builtin_amdgcn_readfirstlane(seq);
