@@ -244,9 +244,7 @@ size_t slot_count(const Plan& p, int num_seqs) {
 WsLayout ws_layout(const Plan& p, int head_dim, int num_seqs) {
   WsLayout w;
   const size_t slots = slot_count(p, num_seqs);
-  w.info = p.stream  ? align_up((size_t)(2 + num_seqs) * sizeof(int))
-           : p.sched ? align_up((size_t)(1 + num_seqs) * sizeof(int))
-                     : 0;
+  w.info = p.stream ? align_up((size_t)(2 + num_seqs) * sizeof(int)) : 0;
   w.ml = align_up(slots * p.head_tile * 2 * sizeof(float));
   w.acc = align_up(slots * p.head_tile * head_dim * sizeof(float));
   w.total = w.info + w.ml + w.acc;

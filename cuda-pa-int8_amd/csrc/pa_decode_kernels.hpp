@@ -57,6 +57,16 @@ constexpr int kThreads = 4 * kWave;   // split-K reduce work-group
 constexpr int kWaitLgkm0 = 0xC07F;
 constexpr float kNegInf = -INFINITY;
 
+// Work-group barrier for LDS traffic only: this thread's LDS accesses are
+// complete (lgkmcnt 0) before it, and, unlike __syncthreads, it waits for no
+// vector-memory operation, so K/V loads already issued stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -825,16 +835,16 @@ __device__ __forceinline__ void merge_wave_states(const Smem& sm, int ct, int nh
 }
 
 // The decode of one split of one unit by a whole work-group.  FUSED:
-// partials are written device-coherent and the last work-group of the unit
-// merges them (single launch).  DIRECT1: a unit with one split writes its
-// output here (else the split-K reduce does).
+// a unit with one split writes its output here; partials are written
+// device-coherent and the last work-group of the unit merges them (single
+// launch).  Otherwise every split writes a partial for the split-K reduce.
 // `after_issue` runs in every wave once the wave's first K/V loads are issued
 // (the scheduled kernel claims its next item there, so that no wait for this
 // split's data also waits for the claim).
 // `resolve(ctx, ns)` supplies the context length and split count once the
 // split's block-id loads are in flight (the grid kernel reads them from
 // memory then) and returns false when the split holds no tokens.
-template <int D, int NW, int CT, bool I8, bool FUSED, bool DIRECT1, bool NTL, bool KNT,
+template <int D, int NW, int CT, bool I8, bool FUSED, bool NTL, bool KNT,
           typename Resolve, typename AfterIssue>
 __device__ __forceinline__ void decode_split(
     const half_t* __restrict__ q, const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc,
@@ -896,10 +906,7 @@ __device__ __forceinline__ void decode_split(
     const int i = tid + k * NW * kWave;
     if (i < nstage) sm.blk[i] = staged[k];
   }
-  // LDS-only barrier: the writes above are complete (lgkmcnt 0) before it,
-  // and no vector-memory wait is implied.
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  __builtin_amdgcn_s_barrier();
+  lds_barrier();   // the block ids above are visible; no wait for the query loads
 
   // ---- software-pipelined token loop: wave w takes chunks w, w + NW, ... of
   // the split.  Once the K rows of its current chunk have fed the QK MFMAs it
@@ -970,7 +977,7 @@ __device__ __forceinline__ void decode_split(
   const size_t slot = wk.slot0 + (size_t)split * wk.stride;
   const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
   const auto rml = buf_rsrc(pml + slot * gt * 2, (uint32_t)(gt * 8));
-  const bool final_here = (FUSED || DIRECT1) && ns_eff == 1;
+  const bool final_here = FUSED && ns_eff == 1;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int nh = min(16, gt - 16 * ct);   // query heads of this tile
@@ -1104,7 +1111,7 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
     ns = ctx > 0 ? (ctx + sh.partition - 1) / sh.partition : 1;
     return split < ns;
   };
-  decode_split<D, NW, CT, I8, FUSED, false, NTL, KNT>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
+  decode_split<D, NW, CT, I8, FUSED, NTL, KNT>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh, wk,
                                              sm, resolve, [] {});
 }
 
@@ -1131,7 +1138,6 @@ decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, PA_SHAPE
 // a split that a sequence does not have, whatever the block-table capacity or
 // the spread of the lengths.
 struct SchedArgs {
-  int* info;          // [1 + num_seqs]: partition, slot row base per sequence (for the reduce)
   uint32_t* queue;    // 8 claim counters, kSchedQueueStride words apart
   int rows_max;       // slot rows the partial buffers hold
   int pmin, pmax;     // partition bounds (multiples of kIterTokens)
@@ -1369,7 +1375,7 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
   return sc;
 }
 
-template <int D, int NW, int CT, bool I8, bool FUSED, bool NTL>
+template <int D, int NW, int CT, bool I8, bool NTL>
 __global__ void __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(2)))
 decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                     PA_SHAPE_HEAD_PARAMS, DecodeShape sh_tail, const half_t* __restrict__ q,
@@ -1441,7 +1447,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                                  : split * P + __builtin_amdgcn_readfirstlane((int)ss.rem[seq]);
     const SplitWork wk{seq, kvh, chunk, split, ctx, P, ns,
                        ((size_t)rowbase * hkv + kvh) * nchunk + chunk, hkv * nchunk};
-    decode_split<D, NW, CT, I8, FUSED, true, NTL, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
+    decode_split<D, NW, CT, I8, true, NTL, false>(q, kc, vc, ksc, vsc, bt, out, pacc, pml, cnt, sh,
                                               wk, sm, [](int&, int&) { return true; }, claim);
     // Every processed item of the class made one claim (the first item of
     // each work-group is static), so the claim that returns items_c - 1 is
@@ -1455,41 +1461,6 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
     __syncthreads();
     idx = __builtin_amdgcn_readfirstlane(ss.next_item);
   }
-  // The split-K reduce reads the partition and the slot row bases.
-  if (!FUSED && blockIdx.x == 0) {
-    if (threadIdx.x == 0) sa.info[0] = P;
-    for (int i = threadIdx.x; i < S; i += NW * kWave) sa.info[1 + i] = ss.full_pre[i] + ss.part_pre[i];
-  }
-}
-
-// Split-K reduce over the in-kernel schedule: one work-group per unit; units
-// with a single split were written by the partition kernel.
-template <int D>
-__global__ void __launch_bounds__(kThreads)
-sched_reduce_kernel(const float* __restrict__ pacc, const float* __restrict__ pml,
-                    const int* __restrict__ ctxl, const int* __restrict__ info,
-                    half_t* __restrict__ out, DecodeShape sh, int rows_max) {
-  const int unit = blockIdx.x;
-  const int chunk = unit % sh.nchunk;
-  const int sk = unit / sh.nchunk;
-  const int kvh = sk % sh.num_kv_heads;
-  const int seq = sk / sh.num_kv_heads;
-  const int cap = sh.max_blocks * sh.block_size;
-  int ctx = ctxl[seq];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int P = info[0];
-  if (P < kIterTokens) return;   // (the partition kernel always writes it)
-  const int ns = ctx > 0 ? (ctx + P - 1) / P : 1;
-  if (ns <= 1) return;
-  const int rb = info[1 + seq];
-  if (rb < 0 || rb > rows_max - ns) return;   // slots stay inside the partial buffers
-  const size_t rowbase = (size_t)rb;
-  const int head0 = kvh * sh.group + chunk * sh.head_tile;
-  const size_t slot0 = (rowbase * sh.num_kv_heads + kvh) * sh.nchunk + chunk;
-  const size_t stride = (size_t)sh.num_kv_heads * sh.nchunk;
-  merge_splits<D, kThreads, false>(
-      pacc, pml, out, [=](int sp) { return slot0 + (size_t)sp * stride; }, sh.head_tile,
-      ((size_t)seq * sh.num_heads + head0) * D, ns);
 }
 
 // ---------------------------------------------------------------------------
@@ -1708,7 +1679,8 @@ decode_stream_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
       nxt = after;
     }
     // ---- the part's end: every wave's state (empty for a wave without a
-    // chunk in it) merges through LDS, column tile by column tile.
+    // chunk in it) merges through LDS, column tile by column tile.  The next
+    // chunk's K/V rows are in flight: the barriers order LDS only.
     const size_t out_base = ((size_t)sg.s * sh.num_heads + head0) * D;
     const size_t slot = 2 * (size_t)blockIdx.x + (seg_lo == A ? 0 : 1);
     const auto racc = buf_rsrc(pacc + slot * gt * D, (uint32_t)(gt * D * 4));
@@ -1716,9 +1688,9 @@ decode_stream_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int nh = min(16, gt - 16 * ct);
-      __syncthreads();   // the previous merge has read the slots
+      lds_barrier();   // the previous merge has read the slots
       dw.store_state(sm, w, ct, nh);
-      __syncthreads();
+      lds_barrier();
       merge_wave_states<D, NW, false>(sm, ct, nh, tid, whole, out, out_base, racc, rml);
     }
     seg_lo = seg_hi;
@@ -1821,25 +1793,15 @@ hipError_t launch_decode_tiles(const DecodeLaunch& l) {
     return hipGetLastError();
   }
   if (l.sched) {
-    const SchedArgs sa{l.sched_info, l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform};
+    const SchedArgs sa{l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform};
     const auto* q = static_cast<const half_t*>(l.q);
     const auto* kc = static_cast<const uint8_t*>(l.k_cache);
     const auto* vc = static_cast<const uint8_t*>(l.v_cache);
     auto* out = static_cast<half_t*>(l.out);
-    if (l.fused) {
-      decode_sched_kernel<D, NW, CT, I8, true, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
-          l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
-          l.part_ml, l.counters, sa);
-      return hipGetLastError();
-    }
-    decode_sched_kernel<D, NW, CT, I8, false, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
-        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales, l.v_scales, out, l.part_acc,
-        l.part_ml, l.counters, sa);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int units = sh.num_seqs * sh.num_kv_heads * sh.nchunk;
-    sched_reduce_kernel<D><<<units, kThreads, 0, l.stream>>>(
-        l.part_acc, l.part_ml, l.context_lens, l.sched_info, out, sh, l.rows_max);
+    // The last work-group of each unit merges its splits in this launch.
+    decode_sched_kernel<D, NW, CT, I8, NTL><<<l.groups, NW * kWave, 0, l.stream>>>(
+        l.block_table, l.context_lens, PA_SHAPE_HEAD_ARGS(sh), sh, q, kc, vc, l.k_scales,
+        l.v_scales, out, l.part_acc, l.part_ml, l.counters, sa);
     return hipGetLastError();
   }
   // Groups of 8 items with their kv heads and head chunks, or, below 8 items,
@@ -1894,9 +1856,9 @@ int resident_query(bool int8_kv, bool stream_part, int* per_cu) {
                       per_cu, decode_stream_kernel<D, NW, CT, false, true>, NW * kWave, 0);
   else
     e = int8_kv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                      per_cu, decode_sched_kernel<D, NW, CT, true, true, true>, NW * kWave, 0)
+                      per_cu, decode_sched_kernel<D, NW, CT, true, true>, NW * kWave, 0)
                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                      per_cu, decode_sched_kernel<D, NW, CT, false, true, true>, NW * kWave, 0);
+                      per_cu, decode_sched_kernel<D, NW, CT, false, true>, NW * kWave, 0);
   return e == hipSuccess ? 0 : -1;
 }
 

@@ -69,6 +69,7 @@ struct DecodeLaunch {
   int waves;           // waves per decode work-group: 4 or 8 (head_dim <= 128)
   bool int8_kv;
   bool fused;          // true: single launch with last-arriver merge; false: partition + reduce
+                       // (the in-kernel schedule is always fused)
   bool nt_loads;       // non-temporal V-row loads (one head chunk per kv head)
   bool k_nt;           // non-temporal K-row loads too (FP16 grid launches, long splits)
   DecodeShape shape;
@@ -83,8 +84,7 @@ struct DecodeLaunch {
   int rows_max;
   int pmin, pmax;      // partition bounds, multiples of 64 (equal when forced)
   int pmin_uniform;    // lower bound for equal lengths (<= pmin)
-  int* sched_info;     // schedule: [1 + num_seqs] partition, then the slot row base of each
-                       // sequence; stream partition: [2 + num_seqs] chunk total, then prefix
+  int* sched_info;     // stream partition: [2 + num_seqs] chunk total, then prefix
   uint32_t* queue;     // 8 claim counters, zero between launches
   hipStream_t stream;
 };
