@@ -138,12 +138,16 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // loss).  The grid and stream forms of split-K keep their reduce launch.
   p.fused = is_fused(kind) || p.sched;
   // Head tile: up to 32 query heads (two MFMA column tiles) for head_dim <=
-  // 128, except under the in-kernel schedule, which keeps 16.  (There, MQA
-  // 32/1 of bench config 5 ran no faster with one 32-head work-group per row
-  // than with two 16-head ones: the rows are too few to balance, 1.3 per
-  // resident work-group; INT8 49.4 -> 56.7 us.)
-  int tile_cap = (head_dim <= 128 && !p.sched) ? pa::kMaxHeadTile : pa::kMaxGroupTile;
-  if (g_head_tile_cap > 0) tile_cap = std::min(tile_cap, g_head_tile_cap);
+  // 128.  Under the in-kernel schedule only for FP16: there the K/V rows of a
+  // kv head are read by one work-group instead of meeting in L2 from two
+  // (MQA 32/1 on 8 x 32k, same box: 45.0 -> 42.9 us; config 5's ragged MQA
+  // about even); INT8 keeps 16, whose single-tile form has the 16-byte W8
+  // loads (8 x 32k INT8: 35.3 us with 16-head tiles, 40.6 with 32).
+  int tile_cap = (head_dim <= 128 && (!p.sched || is_f16(kind))) ? pa::kMaxHeadTile
+                                                                 : pa::kMaxGroupTile;
+  // The hook sets the cap outright (two column tiles need head_dim <= 128).
+  if (g_head_tile_cap > 0)
+    tile_cap = std::min(g_head_tile_cap, head_dim <= 128 ? pa::kMaxHeadTile : pa::kMaxGroupTile);
   p.head_tile = head_tile_for(group, tile_cap);
   p.nchunk = group / p.head_tile;
   p.units = num_seqs * num_kv_heads * p.nchunk;
@@ -224,8 +228,8 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
 
 // Counters (zero between calls): the 8 claim counters of the in-kernel
 // schedule at a fixed offset, then one arrival counter per unit.  Workspace
-// (scratch): the schedule record (in-kernel schedule only), then the split
-// partials.
+// (scratch): the stream partition's chunk record (stream partition only),
+// then the split partials.
 constexpr size_t kQueueBytes = 8 * pa::kSchedQueueStride * sizeof(uint32_t);
 size_t counter_region(int units) {
   return align_up(kQueueBytes) + align_up((size_t)units * sizeof(uint32_t));

@@ -159,20 +159,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 constexpr int kPolicyDevice = 16;
 
 // Folds the partials of splits [0, ns) of one unit, in split order, into the
-// running (max, sum, accumulator) (M, L, A) of item (head h, dims 4c .. 4c +
-// 3); M = -inf: nothing folded yet.  The partial of split sp sits in slot
-// slot_of(sp): acc[gt][D] (relative to its max) and (m, l) per head.  The
-// (m, l) pairs and accumulators of 8 splits at a time are loaded in one batch.
+// running (max, sum, accumulators) (M, L, A) of NI consecutive items of one
+// head: (head h, dims 4(c0 + i) .. 4(c0 + i) + 3), i < NI; M = -inf: nothing
+// folded yet.  The partial of split sp sits in slot slot_of(sp): acc[gt][D]
+// (relative to its max) and (m, l) per head.  SB splits go out as one batch of
+// loads (NI accumulator chunks and one (m, l) pair each), so a unit of ns
+// splits costs ceil(ns / SB) round trips per thread.
 // COHERENT: device-coherent loads (partials written in this launch).
-template <int D, bool COHERENT, typename SlotOf>
+template <int D, bool COHERENT, int NI, int SB, typename SlotOf>
 __device__ __forceinline__ void fold_splits(const float* __restrict__ pacc,
                                             const float* __restrict__ pml, SlotOf slot_of, int gt,
-                                            int h, int c, int ns, float& M, float& L, f4_t& A) {
-  constexpr int SB = 8;
+                                            int h, int c0, int ns, float& M, float& L,
+                                            f4_t (&A)[NI]) {
   constexpr int POL = COHERENT ? kPolicyDevice : 0;
   const uint32_t acc_bytes = (uint32_t)(gt * D * 4), ml_bytes = (uint32_t)(gt * 8);
   for (int s0 = 0; s0 < ns; s0 += SB) {
-    f4_t v[SB];
+    f4_t v[SB][NI];
     f2_t ml[SB];
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
@@ -181,7 +183,10 @@ __device__ __forceinline__ void fold_splits(const float* __restrict__ pacc,
       const size_t slot = slot_of(min(s0 + u, ns - 1));
       const auto ra = buf_rsrc(pacc + slot * gt * D, acc_bytes);
       const auto rm = buf_rsrc(pml + slot * gt * 2, ml_bytes);
-      v[u] = __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * c) * 4, 0, POL));
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        v[u][i] = __builtin_bit_cast(
+            f4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (h * D + 4 * (c0 + i)) * 4, 0, POL));
       ml[u] = __builtin_bit_cast(f2_t, __builtin_amdgcn_raw_buffer_load_b64(rm, h * 8, 0, POL));
     }
     float mb = M;
@@ -189,12 +194,14 @@ __device__ __forceinline__ void fold_splits(const float* __restrict__ pacc,
     for (int u = 0; u < SB; ++u)
       if (s0 + u < ns) mb = fmaxf(mb, ml[u].x);
     const float fo = M == kNegInf ? 0.f : exp2f_fast(M - mb);
-    A *= fo;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) A[i] *= fo;
     L *= fo;
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const float f = (s0 + u < ns && ml[u].x != kNegInf) ? exp2f_fast(ml[u].x - mb) : 0.f;
-      A += v[u] * f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) A[i] += v[u][i] * f;
       L += ml[u].y * f;
     }
     M = mb;
@@ -210,9 +217,38 @@ __device__ __forceinline__ void write_out_item(half_t* __restrict__ out, size_t 
   *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
 }
 
+// Items (head, 4-dim chunk) tid * NI .. + NI - 1, + THREADS * NI, ... of a unit:
+// NI consecutive chunks of one head per thread (D / 4 is a multiple of NI).
+template <int D, int THREADS, bool COHERENT, int NI, int SB, typename SlotOf>
+__device__ __forceinline__ void merge_splits_by(const float* __restrict__ pacc,
+                                                const float* __restrict__ pml,
+                                                half_t* __restrict__ out, SlotOf slot_of, int gt,
+                                                size_t out_base, int ns, int tid) {
+  constexpr int CH = D / 4;
+  static_assert(CH % NI == 0, "a thread's chunks lie in one head");
+  const int nitems = gt * CH;
+  for (int base = tid * NI; base < nitems; base += THREADS * NI) {
+    const int h = base / CH, c0 = base - h * CH;
+    float M = kNegInf, L = 0.f;
+    f4_t A[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) A[i] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    fold_splits<D, COHERENT, NI, SB>(pacc, pml, slot_of, gt, h, c0, ns, M, L, A);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) write_out_item<D>(out, out_base, h, c0 + i, L, A[i]);
+  }
+}
+
 // Merge the `ns` partials of one unit (gt heads) and write its fp16 output
-// rows.  Thread i owns (head, 4-dim chunk) items i, i + THREADS, ... and merges
-// them without LDS or barriers.
+// rows, without LDS or barriers.  With more items than threads each thread
+// takes 2 or 4 consecutive chunks of one head: they share the (m, l) loads,
+// and all of a batch's loads are in flight together (up to about 24 per
+// thread), so the round trips a thread waits for are ceil(ns / SB) rather
+// than one per 8 splits and chunk.  The batch follows ns: the re-read
+// padding of a short last batch costs load slots (config 2, 4 splits: 16-split
+// batches measured 3-4% slower than 4-split ones).  Same box, against one
+// chunk per thread in batches of 8: bench config 3 warp_int8 50.4 -> 48.6
+// us, MQA 32/1 INT8 of config 5 44.8 -> 42.6 us.
 template <int D, int THREADS, bool COHERENT, typename SlotOf>
 __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
                                              const float* __restrict__ pml,
@@ -222,13 +258,27 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));   // nothing lane-dependent is hoisted out of a caller's loop
   const int nitems = gt * CH;
-  for (int i = tid; i < nitems; i += THREADS) {
-    const int h = i / CH, c = i - h * CH;
-    float M = kNegInf, L = 0.f;
-    f4_t A = {0.f, 0.f, 0.f, 0.f};
-    fold_splits<D, COHERENT>(pacc, pml, slot_of, gt, h, c, ns, M, L, A);
-    write_out_item<D>(out, out_base, h, c, L, A);
+#define PA_MERGE_BY(NI, SB) \
+  merge_splits_by<D, THREADS, COHERENT, NI, SB>(pacc, pml, out, slot_of, gt, out_base, ns, tid)
+  if constexpr (CH % 4 == 0) {
+    if (nitems > 2 * THREADS) {
+      if (ns <= 4) PA_MERGE_BY(4, 4);
+      else PA_MERGE_BY(4, 6);
+      return;
+    }
   }
+  if constexpr (CH % 2 == 0) {
+    if (nitems > THREADS) {
+      if (ns <= 4) PA_MERGE_BY(2, 4);
+      else if (ns <= 8 || (ns > 10 && ns <= 16)) PA_MERGE_BY(2, 8);
+      else PA_MERGE_BY(2, 10);
+      return;
+    }
+  }
+  if (ns <= 4) PA_MERGE_BY(1, 4);
+  else if (ns <= 8) PA_MERGE_BY(1, 8);
+  else PA_MERGE_BY(1, 16);
+#undef PA_MERGE_BY
 }
 
 // Block ids of one split: at most max_partition_per_4_waves(D) * NW / 4 tokens,
@@ -1258,9 +1308,10 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
   {
     // P: about one item per CU for equal lengths (per resident work-group
     // with 8-wave groups; with two 4-wave groups per CU, fewer and longer
-    // items measured faster: config 4 32k INT8 93.6 -> 91.8 us), about
-    // kSchedItemsPerGroup per work-group otherwise; within [pmin, pmax] and
-    // no longer than the longest sequence.
+    // items measured faster: config 4 32k INT8 93.6 -> 91.8 us, and every
+    // extra split is merged at the end), about kSchedItemsPerGroup per
+    // work-group otherwise; within [pmin, pmax] and no longer than the
+    // longest sequence.
     constexpr uint64_t kGroupsPerCU = kWavesPerCU / NWV;
     const uint64_t groups = sc.uniform ? (gridDim.x + kGroupsPerCU - 1) / kGroupsPerCU : gridDim.x;
     const uint64_t k = sc.uniform ? 1 : kSchedItemsPerGroup;
