@@ -609,7 +609,7 @@ pa_status_t quant_write(const void* key, const void* value, int64_t key_token_st
                         int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
                         void* k_cache, void* v_cache, float* k_scales, float* v_scales,
                         const float* k_scale_in, const float* v_scale_in, int32_t num_blocks,
-                        int32_t block_size, int32_t x, pa_stream_t stream) {
+                        int32_t block_size, int32_t x, pa_stream_t stream, bool bf16_input) {
   const pa_status_t st = check_write_args(
       key, value, key_token_stride, key_head_stride, value_token_stride, value_head_stride,
       slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache, v_cache, num_blocks, block_size,
@@ -635,6 +635,7 @@ pa_status_t quant_write(const void* key, const void* value, int64_t key_token_st
   l.v_scale_in = v_scale_in;
   l.num_blocks = num_blocks;
   l.block_size = block_size;
+  l.bf16_input = bf16_input;
   l.stream = reinterpret_cast<hipStream_t>(stream);
   return pa::launch_quant_write_i8(l) == hipSuccess ? PA_OK : PA_ERR_LAUNCH;
 }
@@ -654,7 +655,21 @@ pa_status_t pa_reshape_and_cache_int8(const void* key, const void* value,
   return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
                      value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
                      v_cache, k_scales, v_scales, nullptr, nullptr, num_blocks, block_size, x,
-                     stream);
+                     stream, false);
+}
+
+pa_status_t pa_reshape_and_cache_int8_bf16(const void* key, const void* value,
+                                           int64_t key_token_stride, int64_t key_head_stride,
+                                           int64_t value_token_stride, int64_t value_head_stride,
+                                           const int64_t* slot_mapping, int32_t num_tokens,
+                                           int32_t num_kv_heads, int32_t head_dim, void* k_cache,
+                                           void* v_cache, float* k_scales, float* v_scales,
+                                           int32_t num_blocks, int32_t block_size, int32_t x,
+                                           pa_stream_t stream) {
+  return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
+                     value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
+                     v_cache, k_scales, v_scales, nullptr, nullptr, num_blocks, block_size, x,
+                     stream, true);
 }
 
 pa_status_t pa_reshape_and_cache_int8_static(
@@ -667,7 +682,20 @@ pa_status_t pa_reshape_and_cache_int8_static(
   return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
                      value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
                      v_cache, k_scales, v_scales, k_scale, v_scale, num_blocks, block_size, x,
-                     stream);
+                     stream, false);
+}
+
+pa_status_t pa_reshape_and_cache_int8_static_bf16(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim, void* k_cache, void* v_cache,
+    float* k_scales, float* v_scales, const float* k_scale, const float* v_scale,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream) {
+  if (num_tokens > 0 && (!k_scale || !v_scale)) return PA_ERR_NULL_POINTER;
+  return quant_write(key, value, key_token_stride, key_head_stride, value_token_stride,
+                     value_head_stride, slot_mapping, num_tokens, num_kv_heads, head_dim, k_cache,
+                     v_cache, k_scales, v_scales, k_scale, v_scale, num_blocks, block_size, x,
+                     stream, true);
 }
 
 pa_status_t pa_reshape_and_cache_f16(const void* key, const void* value,

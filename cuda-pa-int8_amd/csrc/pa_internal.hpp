@@ -165,6 +165,7 @@ struct QuantLaunch {
   const float* v_scale_in;
   int num_blocks;
   int block_size;
+  bool bf16_input;   // key / value are bf16 (else fp16)
   hipStream_t stream;
 };
 

@@ -2,8 +2,9 @@
 //
 // Semantics (bit-exact with the reference's torch code):
 //   quantize_per_token, tests/paged_decode_attn.py:106-112
-//     amax  = max_d |x_d|                 (in fp16, exact)
-//     scale = fp32(fp16(max(amax, 1e-8) / 127))   (fp16 division rounded once)
+//     amax  = max_d |x_d|                 (in the input type, exact)
+//     scale = fp32(t(max(amax, t(1e-8)) / 127))   (t = fp16 or bf16, the input
+//                                                  type; the division rounded once)
 //     q_d   = int8(clamp(rne(fp32(x_d) / scale), -127, 127)), NaN -> 0
 //   placement, tests/paged_decode_attn.py:190-197 and
 //   benchmarks/int8_bridge/paged_cache.py:145-154
@@ -55,6 +56,27 @@ constexpr float kRoundMagic = 12582912.0f;   // 1.5 * 2^23: y + magic rounds y t
 // (checked exhaustively on the CPU).
 constexpr float kInv127 = 1.0f / 127.0f;
 
+// The two elements of a 32-bit word of fp16 (BF false) or bf16 (BF true)
+// input, widened to fp32 (exactly).
+template <bool BF>
+__device__ __forceinline__ void widen2(uint32_t w, float& lo, float& hi) {
+  if constexpr (BF) {
+    lo = __builtin_bit_cast(float, w << 16);
+    hi = __builtin_bit_cast(float, w & 0xFFFF0000u);
+  } else {
+    const half2_t h = __builtin_bit_cast(half2_t, w);
+    lo = (float)h.x;
+    hi = (float)h.y;
+  }
+}
+
+// fp32 -> bf16 -> fp32, round to nearest even; a NaN stays a (quiet) NaN.
+__device__ __forceinline__ float round_bf16(float f) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  const uint32_t r = (f != f) ? ((b >> 16) | 0x40u) : ((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+  return __builtin_bit_cast(float, r << 16);
+}
+
 // Exact path: rne(x / s) with IEEE division, clamped to [-127, 127], NaN -> 0.
 __device__ __forceinline__ uint32_t quant_exact_byte(float x, float s) {
   float r = __builtin_rintf(x / s);
@@ -70,14 +92,15 @@ __device__ __forceinline__ uint32_t quant_exact_byte(float x, float s) {
 // no range check is needed, and the inputs are finite (a NaN or inf in the row
 // makes the scale non-normal, which takes the exact path): the largest
 // distance to an integer over the group decides with one comparison.
+template <bool BF>
 __device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow) {
   const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t bytes[8];
   float dmax = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
-    const float xs[2] = {(float)h.x, (float)h.y};
+    float xs[2];
+    widen2<BF>(wv[k], xs[0], xs[1]);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const float y = xs[e] * r;
@@ -99,13 +122,14 @@ __device__ __forceinline__ uint2 quant_group_fast(uint4 xv, float r, bool& slow)
 // +-127 (the IEEE quotient then exceeds 126.5, the reciprocal being a normal
 // number, so it rounds to >= 127 and clamps there); the rest lies below 127
 // and rounds as above.
+template <bool BF>
 __device__ __forceinline__ uint2 quant_group_fast_sat(uint4 xv, float r, bool& slow) {
   const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t bytes[8];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
-    const float xs[2] = {(float)h.x, (float)h.y};
+    float xs[2];
+    widen2<BF>(wv[k], xs[0], xs[1]);
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const float y = xs[e] * r;
@@ -124,14 +148,16 @@ __device__ __forceinline__ uint2 quant_group_fast_sat(uint4 xv, float r, bool& s
 }
 
 // The exact path for one 16-B group.
+template <bool BF>
 __device__ __forceinline__ uint2 quant_group_exact(uint4 xv, float s) {
   const uint32_t wv[4] = {xv.x, xv.y, xv.z, xv.w};
   uint32_t b[8];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const half2_t h = __builtin_bit_cast(half2_t, wv[k]);
-    b[2 * k] = quant_exact_byte((float)h.x, s);
-    b[2 * k + 1] = quant_exact_byte((float)h.y, s);
+    float lo, hi;
+    widen2<BF>(wv[k], lo, hi);
+    b[2 * k] = quant_exact_byte(lo, s);
+    b[2 * k + 1] = quant_exact_byte(hi, s);
   }
   return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
                     b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
@@ -164,9 +190,10 @@ struct QuantJob {
 
 // STATIC: every K element is quantized with *k_scale_in and every V element
 // with *v_scale_in (the per-tensor mode), instead of its token's own scale.
-template <int D, bool STATIC>
+// BF: the inputs are bf16 (bit patterns) instead of fp16.
+template <int D, bool STATIC, bool BF>
 __global__ void __launch_bounds__(kQuantWaves * kWave)
-quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ value, int64_t kts,
+quant_write_kernel(const uint16_t* __restrict__ key, const uint16_t* __restrict__ value, int64_t kts,
                    int64_t khs, int64_t vts, int64_t vhs, const int64_t* __restrict__ slots,
                    int num_tokens, int num_kv_heads, int8_t* __restrict__ kc,
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
@@ -195,8 +222,8 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     const int tok = (th / num_kv_heads) * 16 + i;
     const int tc = tok < num_tokens ? tok : num_tokens - 1;
     J.slot = slots[tc];
-    const half_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
-                             : key + (int64_t)tc * kts + (int64_t)h * khs;
+    const uint16_t* src = is_v ? value + (int64_t)tc * vts + (int64_t)h * vhs
+                               : key + (int64_t)tc * kts + (int64_t)h * khs;
 #pragma unroll
     for (int j = 0; j < JQ; ++j) {
       const int o = qq + 4 * j < DG ? qq + 4 * j : DG - 1;
@@ -233,9 +260,9 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       const float rr = 1.0f / s;
       s_normal = rr >= 1.17549435e-38f && rr <= 3.40282347e+38f;
     } else {
-      // amax over the token's D values as fp16 magnitude bits (ordered like the
-      // values; a NaN input gives NaN bits above +inf, so the scale becomes NaN
-      // as in torch).
+      // amax over the token's D values as fp16 / bf16 magnitude bits (ordered
+      // like the values; a NaN input gives NaN bits above +inf, so the scale
+      // becomes NaN as in torch).
       u16x2_t am2 = {0, 0};
 #pragma unroll
       for (int j = 0; j < JQ; ++j) {
@@ -247,12 +274,24 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
       }
       uint32_t am = am2[0] > am2[1] ? am2[0] : am2[1];
       am = rows_umax(am);
-      const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
-      const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
-      s = (float)(half_t)(a * kInv127);                   // == fp16(a / 127), RNE
-      // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
-      // sends the token's elements to the exact path.
-      s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
+      if constexpr (BF) {
+        // bf16: amax and clamp_min(bf16(1e-8)) are exact in fp32; the quotient
+        // is the IEEE one rounded to bf16 (one rounding, as torch's).
+        const float amax = __builtin_bit_cast(float, am << 16);
+        const float lo = __builtin_bit_cast(float, 0x322C0000u);   // bf16(1e-8), RNE
+        const float a = (amax < lo) ? lo : amax;             // clamp_min, NaN-preserving
+        s = round_bf16(a / 127.f);
+        // bf16 keeps fp32's exponent range: only NaN / inf leave the fast path
+        // (a normal bf16 scale keeps |x / s| <= 127 (1 + 2^-8) < 127.5).
+        s_normal = s >= 1.17549435e-38f && s <= 3.38953139e+38f;
+      } else {
+        const float amax = (float)__builtin_bit_cast(half_t, (uint16_t)am);
+        const float a = (amax < 1e-8f) ? 1e-8f : amax;      // clamp_min, NaN-preserving
+        s = (float)(half_t)(a * kInv127);                   // == fp16(a / 127), RNE
+        // A scale that is not a normal fp16 number (zero, subnormal, NaN, inf)
+        // sends the token's elements to the exact path.
+        s_normal = s >= 6.103515625e-05f && s <= 65504.0f;
+      }
     }
     // Per-token scales are normal fp16 numbers on the fast path, so the
     // hardware reciprocal is finite and within the guard's error budget; a
@@ -284,10 +323,10 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
     for (int j = 0; j < JQ; ++j) {
       if (qq + 4 * j >= DG) continue;   // padding group: nothing to write
       bool slow = !s_normal;
-      uint2 qj = STATIC ? quant_group_fast_sat(cur.x[j], r, slow)
-                        : quant_group_fast(cur.x[j], r, slow);
+      uint2 qj = STATIC ? quant_group_fast_sat<BF>(cur.x[j], r, slow)
+                        : quant_group_fast<BF>(cur.x[j], r, slow);
       if (__builtin_amdgcn_ballot_w64(slow) != 0) {
-        if (slow) qj = quant_group_exact(cur.x[j], s);   // rare: the reference's division
+        if (slow) qj = quant_group_exact<BF>(cur.x[j], s);   // rare: the reference's division
       }
       const int o = qq + 4 * j;   // dim group: dims 8o .. 8o+7
       if (!is_v) {
@@ -347,7 +386,7 @@ quant_write_kernel(const half_t* __restrict__ key, const half_t* __restrict__ va
 
 // Work-groups the GPU holds at once for this kernel: the grid-stride loop is
 // sized to them so that no group starts after the others have finished.
-template <int D, bool STATIC>
+template <int D, bool STATIC, bool BF>
 int resident_groups() {
   static int cache[64] = {0};
   int dev = 0;
@@ -357,7 +396,7 @@ int resident_groups() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quant_write_kernel<D, STATIC>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quant_write_kernel<D, STATIC, BF>,
                                                      kQuantWaves * kWave, 0) != hipSuccess ||
         per_cu <= 0)
       per_cu = 4;
@@ -366,14 +405,14 @@ int resident_groups() {
   return cache[dev];
 }
 
-template <int D, bool STATIC>
+template <int D, bool STATIC, bool BF>
 static hipError_t launch_quant_d(const QuantLaunch& l) {
   const int tiles = (l.num_tokens + 15) / 16;
   const int njobs = tiles * l.num_kv_heads * 2;
   const int want = (njobs + kQuantWaves - 1) / kQuantWaves;
-  const int grid = std::min(want, resident_groups<D, STATIC>());
-  quant_write_kernel<D, STATIC><<<grid, kQuantWaves * kWave, 0, l.stream>>>(
-      static_cast<const half_t*>(l.key), static_cast<const half_t*>(l.value), l.key_token_stride,
+  const int grid = std::min(want, resident_groups<D, STATIC, BF>());
+  quant_write_kernel<D, STATIC, BF><<<grid, kQuantWaves * kWave, 0, l.stream>>>(
+      static_cast<const uint16_t*>(l.key), static_cast<const uint16_t*>(l.value), l.key_token_stride,
       l.key_head_stride, l.value_token_stride, l.value_head_stride, l.slot_mapping, l.num_tokens,
       l.num_kv_heads, static_cast<int8_t*>(l.k_cache), static_cast<int8_t*>(l.v_cache),
       l.k_scales, l.v_scales, l.num_blocks, l.block_size, __builtin_ctz((unsigned)l.block_size),
@@ -381,11 +420,11 @@ static hipError_t launch_quant_d(const QuantLaunch& l) {
   return hipGetLastError();
 }
 
-template <bool STATIC>
+template <bool STATIC, bool BF>
 static hipError_t launch_quant(const QuantLaunch& l) {
   switch (l.head_dim) {
 #define PA_CASE(D) \
-  case D: return launch_quant_d<D, STATIC>(l);
+  case D: return launch_quant_d<D, STATIC, BF>(l);
     PA_FOR_EACH_HEAD_DIM(PA_CASE)
 #undef PA_CASE
     default: return hipErrorInvalidValue;
@@ -393,7 +432,9 @@ static hipError_t launch_quant(const QuantLaunch& l) {
 }
 
 hipError_t launch_quant_write_i8(const QuantLaunch& l) {
-  return (l.k_scale_in != nullptr) ? launch_quant<true>(l) : launch_quant<false>(l);
+  if (l.bf16_input)
+    return (l.k_scale_in != nullptr) ? launch_quant<true, true>(l) : launch_quant<false, true>(l);
+  return (l.k_scale_in != nullptr) ? launch_quant<true, false>(l) : launch_quant<false, false>(l);
 }
 
 }  // namespace pa

@@ -284,8 +284,14 @@ void check_write(const at::Tensor& key, const at::Tensor& value, const at::Tenso
                  const at::Tensor& v_cache, const at::Tensor* k_scales,
                  const at::Tensor* v_scales, const at::Tensor& slot_mapping, bool int8) {
   TORCH_CHECK(key.is_cuda() && value.is_cuda(), "tensors must be on CUDA");
-  TORCH_CHECK(key.scalar_type() == at::kHalf && value.scalar_type() == at::kHalf,
-              "key and value must be fp16");
+  if (int8) {
+    TORCH_CHECK((key.scalar_type() == at::kHalf || key.scalar_type() == at::kBFloat16) &&
+                    value.scalar_type() == key.scalar_type(),
+                "key and value must be fp16 or bf16 (the same)");
+  } else {
+    TORCH_CHECK(key.scalar_type() == at::kHalf && value.scalar_type() == at::kHalf,
+                "key and value must be fp16");
+  }
   if (int8) {
     TORCH_CHECK(k_cache.scalar_type() == at::kChar && v_cache.scalar_type() == at::kChar,
                 "k_cache and v_cache must be int8");
@@ -320,14 +326,16 @@ void check_write(const at::Tensor& key, const at::Tensor& value, const at::Tenso
   }
 }
 
-// NEW op (no reference counterpart): per-token INT8 quantize + paged write.
+// NEW op (no reference counterpart): per-token INT8 quantize + paged write
+// of fp16 or bf16 key / value.
 void reshape_and_cache_int8(at::Tensor key, at::Tensor value, at::Tensor k_cache,
                             at::Tensor v_cache, at::Tensor k_scales, at::Tensor v_scales,
                             at::Tensor slot_mapping) {
   check_write(key, value, k_cache, v_cache, &k_scales, &v_scales, slot_mapping, true);
   const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
-  check_status(pa_reshape_and_cache_int8(
+  const bool bf = key.scalar_type() == at::kBFloat16;
+  check_status((bf ? pa_reshape_and_cache_int8_bf16 : pa_reshape_and_cache_int8)(
       key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
       value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)key.size(0),
       (int32_t)key.size(1), (int32_t)key.size(2), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -349,7 +357,8 @@ void reshape_and_cache_int8_static(at::Tensor key, at::Tensor value, at::Tensor 
                 "k_scale and v_scale must be one fp32 value each on key's device");
   const at::hip::HIPGuardMasqueradingAsCUDA guard(key.device());
   hipStream_t stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(key.get_device()).stream();
-  check_status(pa_reshape_and_cache_int8_static(
+  const bool bf = key.scalar_type() == at::kBFloat16;
+  check_status((bf ? pa_reshape_and_cache_int8_static_bf16 : pa_reshape_and_cache_int8_static)(
       key.data_ptr(), value.data_ptr(), key.stride(0), key.stride(1), value.stride(0),
       value.stride(1), slot_mapping.data_ptr<int64_t>(), (int32_t)key.size(0),
       (int32_t)key.size(1), (int32_t)key.size(2), k_cache.data_ptr(), v_cache.data_ptr(),

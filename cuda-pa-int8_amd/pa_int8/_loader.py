@@ -103,6 +103,12 @@ PROTOTYPES = {
     "pa_reshape_and_cache_int8_static": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p,
                                                         _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                                         _p, _i32, _i32, _i32, _p]),
+    "pa_reshape_and_cache_int8_bf16": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32,
+                                                      _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32,
+                                                      _p]),
+    "pa_reshape_and_cache_int8_static_bf16": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p,
+                                                             _i32, _i32, _i32, _p, _p, _p, _p, _p,
+                                                             _p, _i32, _i32, _i32, _p]),
     "pa_reshape_and_cache_f16": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32,
                                                 _i32, _p, _p, _i32, _i32, _i32, _p]),
 }

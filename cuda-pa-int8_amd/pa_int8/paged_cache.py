@@ -18,8 +18,10 @@ Where the reference quantizes with several torch ops and scatters with
 permuted copies, each write here is one kernel launch; the per-tensor amax
 is a torch reduction on the device.  ``prefill`` also clears the unused tail
 of the last block, as the reference's zero-padded copy does (:116-128).
-Writes need fp16 K/V on a HIP device (the kernels' input type); the fp16
-variant converts other float dtypes first, as the reference does (:111).
+Writes take fp16 K/V on a HIP device, and the INT8 variants bf16 too (the
+dtype the reference's bridge runs Qwen in, quantized directly as its
+quantize_per_token does); the fp16 variant converts other float dtypes first,
+as the reference does (:111).
 """
 
 from __future__ import annotations
@@ -76,8 +78,9 @@ class PagedKVCache:
     def _kernel_input(self, t):
         if self.variant == "fp16" and t.dtype != torch.float16:
             t = t.to(torch.float16)
-        if t.dtype != torch.float16:
-            raise TypeError(f"PagedKVCache({self.variant!r}) writes fp16 K/V; got {t.dtype}")
+        if t.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"PagedKVCache({self.variant!r}) writes fp16 or bf16 K/V; "
+                            f"got {t.dtype}")
         if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
             t = t.contiguous()
         return t

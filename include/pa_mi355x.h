@@ -228,6 +228,27 @@ pa_status_t pa_reshape_and_cache_int8_static(
     const float* k_scale, const float* v_scale,
     int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
 
+/* The two writes above with bfloat16 key / value (bit patterns, same shapes
+ * and strides).  NEW API: the reference's quantize_per_token on a bf16 tensor
+ * (tests/paged_decode_attn.py:106-112, the dtype its bridge runs Qwen in,
+ * benchmarks/int8_bridge/run_bridge.py:99): amax and clamp_min(1e-8) in bf16,
+ * scale = fp32(bf16(amax / 127)), q = int8(clamp(rne(fp32(x) / scale), -127,
+ * 127)).  The per-tensor form takes the caller's fp32 scales as
+ * pa_reshape_and_cache_int8_static does. */
+pa_status_t pa_reshape_and_cache_int8_bf16(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    void* k_cache, void* v_cache, float* k_scales, float* v_scales,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
+pa_status_t pa_reshape_and_cache_int8_static_bf16(
+    const void* key, const void* value, int64_t key_token_stride, int64_t key_head_stride,
+    int64_t value_token_stride, int64_t value_head_stride, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    void* k_cache, void* v_cache, float* k_scales, float* v_scales,
+    const float* k_scale, const float* v_scale,
+    int32_t num_blocks, int32_t block_size, int32_t x, pa_stream_t stream);
+
 /* FP16 paged-cache write (no quantization).  NEW API (the reference scatters
  * with torch indexing): the "fp16" write path of PagedKVCache
  * (benchmarks/int8_bridge/paged_cache.py:116-130 prefill, :148-150

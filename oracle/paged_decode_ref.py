@@ -21,9 +21,12 @@ Yevsquant/cuda-PA-INT8) in vectorised numpy:
                                  (slot = block * block_size + offset)
 * ``reshape_and_cache_int8_static``  the per-tensor write of
                                  benchmarks/int8_bridge/paged_cache.py:99-106,140-142
+* ``reshape_and_cache_int8_bf16``, ``reshape_and_cache_int8_static_bf16``
+                                 the two writes on bfloat16 input (bit patterns)
 * ``reshape_and_cache_f16``      the fp16 write of paged_cache.py:116-130,148-150
                                  (placement of tests/paged_decode_attn.py:85-99)
 * ``paged_cache_tensor_scale``   benchmarks/int8_bridge/paged_cache.py:101-102
+                                 (``paged_cache_tensor_scale_bf16`` on bfloat16 input)
 * ``dense_attention``            tests/test_paged_decode_attn.py:37-52
 
 How each one is pinned (checked against something other than itself) is
@@ -413,6 +416,34 @@ def reshape_and_cache_int8_static(key, value, slot_mapping, k_cache, v_cache, k_
     ks = np.full((t_, hkv), np.float32(k_scale), np.float32)
     vs = np.full((t_, hkv), np.float32(v_scale), np.float32)
     _place(slot_mapping, k_cache, v_cache, kq, vq, k_scales, v_scales, ks, vs)
+
+
+def reshape_and_cache_int8_bf16(key_bits, value_bits, slot_mapping, k_cache, v_cache,
+                                k_scales, v_scales):
+    """``reshape_and_cache_int8`` on bfloat16 ``key/value [T, Hkv, D]`` given as
+    bit patterns: ``quantize_per_token_bf16`` per (token, kv head), the same
+    placement."""
+    kq, ks = quantize_per_token_bf16(key_bits, axis=-1)
+    vq, vs = quantize_per_token_bf16(value_bits, axis=-1)
+    _place(slot_mapping, k_cache, v_cache, kq, vq, k_scales, v_scales, ks, vs)
+
+
+def reshape_and_cache_int8_static_bf16(key_bits, value_bits, slot_mapping, k_cache, v_cache,
+                                       k_scales, v_scales, k_scale, v_scale):
+    """``reshape_and_cache_int8_static`` on bfloat16 input (bit patterns): the
+    values widen exactly to float32 before the division."""
+    reshape_and_cache_int8_static(bf16_bits_to_f32(key_bits), bf16_bits_to_f32(value_bits),
+                                  slot_mapping, k_cache, v_cache, k_scales, v_scales, k_scale,
+                                  v_scale)
+
+
+def paged_cache_tensor_scale_bf16(bits):
+    """``paged_cache_tensor_scale`` on a bfloat16 tensor (bit patterns): amax
+    exact, the division by 127 rounded once to bfloat16 (as torch computes a
+    bfloat16 quotient), then float32 and the clamp."""
+    amax = np.abs(bf16_bits_to_f32(bits)).max()
+    s = bf16_bits_to_f32(f32_to_bf16_bits(np.float32(amax) / np.float32(127.0)))
+    return np.float32(max(np.float32(s), np.float32(1e-8)))
 
 
 def reshape_and_cache_f16(key, value, slot_mapping, k_cache, v_cache):

@@ -172,6 +172,46 @@ def test_quant_per_token_matches_reference_golden_bf16():
     assert np.array_equal(s[fin].view(np.uint32), z["sb16"][fin].view(np.uint32))
 
 
+def test_paged_cache_tensor_scale_bf16_matches_torch():
+    """The per-tensor scale of PagedKVCache.prefill on bf16 K/V
+    (benchmarks/int8_bridge/paged_cache.py:101-102) evaluated by torch's own
+    bfloat16 arithmetic on the CPU: amax, the bf16 quotient, float32, clamp."""
+    rng = np.random.default_rng(21)
+    cases = [rng.standard_normal((7, 2, 64)).astype(np.float32) * sc for sc in (1e-12, 3e-9, 1.0, 3e4)]
+    cases.append(np.zeros((3, 2, 64), np.float32))
+    import torch
+
+    for x in cases:
+        bits = ref.f32_to_bf16_bits(x)
+        t = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+        want = (t.abs().amax() / 127.0).to(torch.float32).clamp_min(1e-8).item()
+        got = ref.paged_cache_tensor_scale_bf16(bits)
+        assert np.float32(want).view(np.uint32) == np.float32(got).view(np.uint32)
+
+
+def test_reshape_and_cache_int8_bf16_places_golden_rows():
+    """The bf16 write places quantize_per_token_bf16's rows of the golden
+    fixture (reference-written) at their slots; untouched slots keep their
+    bytes."""
+    z = _golden()
+    x = z["xb16_bits"]                                  # [R, 128] bf16 bits
+    R, d = x.shape
+    bs, nb = 16, 4
+    rng = np.random.default_rng(3)
+    slots = rng.permutation(nb * bs)[:R].astype(np.int64)
+    kc = np.full((nb, 1, d // 8, bs, 8), 5, np.int8); vc = np.full((nb, 1, d, bs), 5, np.int8)
+    ks = np.full((nb, 1, bs), 7.0, np.float32); vs = ks.copy()
+    ref.reshape_and_cache_int8_bf16(x[:, None], x[::-1, None].copy(), slots, kc, vc, ks, vs)
+    blk, off = slots // bs, slots % bs
+    assert np.array_equal(kc[blk, 0, :, off, :].reshape(R, d), z["qb16"])
+    assert np.array_equal(vc[blk, 0, :, off], z["qb16"][::-1])
+    got = ks[blk, 0, off]
+    fin = ~np.isnan(z["sb16"])
+    assert np.array_equal(got[fin].view(np.uint32), z["sb16"][fin].view(np.uint32))
+    free = np.setdiff1d(np.arange(nb * bs), slots)
+    assert (kc[free // bs, 0, :, free % bs, :] == 5).all() and (ks[free // bs, 0, free % bs] == 7).all()
+
+
 def test_bf16_rounding_helpers():
     """f32 -> bf16 bit rounding agrees with torch's conversion on every bf16
     neighbourhood we can name: exact values, midpoints (ties to even), and
