@@ -573,6 +573,64 @@ def steps_for(us_est, cap):
     return int(max(10, min(cap, 40_000 // max(1, us_est))))
 
 
+def run_cfg5_counter_launches(torch, launches=8):
+    """Config 5's four decode launches (32/8 and MQA 32/1, FP16 and INT8) for
+    counter collection under rocprofv3 --pmc: plain launches, no timing and no
+    gate.  The cases are built without torch index kernels: the block table
+    and slot mapping are made on the host, and each INT8 cache is written by
+    one call of the write kernel."""
+    import math
+
+    import numpy as np
+
+    import pa_int8
+
+    dev, bs, d = "cuda", 16, 128
+    lens = lognormal_lens(256, seed=5)
+    rng = np.random.default_rng(5)
+    nblk = [(n + bs - 1) // bs for n in lens]
+    nb = sum(nblk) + 1
+    perm = rng.permutation(nb).astype(np.int32)
+    bt_np = np.zeros((len(lens), max(nblk)), np.int32)
+    off = 0
+    for s_, k in enumerate(nblk):
+        bt_np[s_, :k] = perm[off:off + k]
+        off += k
+    slots = np.concatenate([bt_np[s_, np.arange(n) // bs].astype(np.int64) * bs + np.arange(n) % bs
+                            for s_, n in enumerate(lens)])
+    bt, ctx = torch.from_numpy(bt_np).to(dev), torch.tensor(lens, dtype=torch.int32).to(dev)
+    slots_t, T = torch.from_numpy(slots).to(dev), int(sum(lens))
+    done = []
+    for hkv in (8, 1):
+        q = torch.randn((len(lens), 32, d), dtype=torch.float16, device=dev)
+        out = torch.empty_like(q)
+        for int8 in (False, True):
+            if int8:
+                kc = torch.zeros((nb, hkv, d // 8, bs, 8), dtype=torch.int8, device=dev)
+                vc = torch.zeros((nb, hkv, d, bs), dtype=torch.int8, device=dev)
+                ks = torch.zeros((nb, hkv, bs), dtype=torch.float32, device=dev)
+                vs = torch.zeros_like(ks)
+                k = torch.randn((T, hkv, d), dtype=torch.float16, device=dev)
+                v = torch.randn((T, hkv, d), dtype=torch.float16, device=dev)
+                pa_int8.reshape_and_cache_int8(k, v, kc, vc, ks, vs, slots_t)
+                del k, v
+                kw, variant = dict(k_scales=ks, v_scales=vs), "splitk_int8"
+            else:
+                kc = torch.randn((nb, hkv, d // 8, bs, 8), dtype=torch.float16, device=dev)
+                vc = torch.randn((nb, hkv, d, bs), dtype=torch.float16, device=dev)
+                kw, variant = {}, "splitk"
+            torch.cuda.synchronize()
+            for _ in range(launches):
+                pa_int8.decode(variant, out, q, kc, vc, bt, ctx, 1.0 / math.sqrt(d), bs,
+                               check=False, **kw)
+            torch.cuda.synchronize()
+            done.append(f"32/{hkv} {variant} x{launches}")
+            log(f"[bench] cfg5 counter launches: 32/{hkv} {variant} x{launches}")
+            del kc, vc, kw
+            torch.cuda.empty_cache()
+    return dict(launches=done, note="plain launches for rocprofv3 counters; not timed")
+
+
 def run_configs(torch, names, steps, warmup):
     import numpy as np
 
@@ -610,6 +668,8 @@ def run_configs(torch, names, steps, warmup):
         out["cfg5_lens"] = dict(n=256, median=int(np.median(lens)), mean=float(np.mean(lens)),
                                 max=int(max(lens)), sigma=1.0,
                                 distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
+    if "cfg5counters" in names:
+        out["cfg5_counter_launches"] = run_cfg5_counter_launches(torch)
     if "refshapes" in names:
         rows = []
         for b, ctx, h, hkv, variant, a100_us, src in REF_SHAPES:
@@ -797,7 +857,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="all",
-                    help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'")
+                    help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'; also "
+                    "cfg5counters (config 5's decode launches for rocprofv3 counters, untimed)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
