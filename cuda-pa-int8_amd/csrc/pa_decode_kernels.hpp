@@ -1199,7 +1199,7 @@ constexpr int kShortBuckets = 4;   // (their counts pack into one 64-bit word)
 struct SchedSmem {
   int full_pre[kSchedMaxSeqs + 1];        // exclusive prefix of full rows per sequence
   uint16_t part_pre[kSchedMaxSeqs + 1];   // exclusive prefix of short last rows (<= S)
-  uint16_t rem[kSchedMaxSeqs];            // context length % P (P <= 8192)
+  uint16_t rem[kSchedMaxSeqs];            // context length % P (P <= 16384)
   uint16_t short_seq[kSchedMaxSeqs];      // sequence of short row j (longest first)
   uint64_t band_scan[16];                 // per-wave totals of the band counts
   uint32_t red[3][16];               // per-wave sum (in 1024-token units), min, max
@@ -1262,6 +1262,32 @@ struct Schedule {
   bool uniform;
 };
 
+// Unsigned division by a divisor fixed for many dividends (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994,
+// fig. 4.1): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+// n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0), t = mulhi(m, n),
+// exact for every 32-bit n and 1 <= d < 2^31.  The setup runs once per
+// divisor (uniform, on the scalar unit); each quotient costs a multiply-high,
+// a subtraction, an add and two shifts instead of a division sequence.
+struct DivU32 {
+  uint32_t m;
+  int s1, s2;
+  uint32_t d;
+};
+__device__ __forceinline__ DivU32 div_setup(uint32_t d) {
+  const int l = d > 1 ? 32 - __builtin_clz(d - 1) : 0;   // ceil(log2 d)
+  DivU32 v;
+  v.m = (uint32_t)((((1ull << l) - d) << 32) / d + 1);
+  v.s1 = l < 1 ? l : 1;
+  v.s2 = l - 1 > 0 ? l - 1 : 0;
+  v.d = d;
+  return v;
+}
+__device__ __forceinline__ uint32_t div_q(const DivU32& v, uint32_t n) {
+  const uint32_t t = __umulhi(v.m, n);
+  return (t + ((n - t) >> v.s1)) >> v.s2;
+}
+
 // Builds the schedule in LDS; every thread of the work-group takes part and
 // returns the same values.  Thread t owns sequences [t*E, t*E + E).
 template <int NTH>
@@ -1315,7 +1341,11 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
     constexpr uint64_t kGroupsPerCU = kWavesPerCU / NWV;
     const uint64_t groups = sc.uniform ? (gridDim.x + kGroupsPerCU - 1) / kGroupsPerCU : gridDim.x;
     const uint64_t k = sc.uniform ? 1 : kSchedItemsPerGroup;
-    uint64_t part = ((t << 10) * (uint64_t)sh.num_kv_heads + groups * k - 1) / (groups * k);
+    // (in float: a 64-bit integer division is a long scalar sequence, and
+    // every work-group evaluates the same operations on the same values)
+    const float want = __builtin_ceilf((float)t * (1024.f * (float)sh.num_kv_heads) /
+                                       (float)(groups * k));
+    uint64_t part = (uint64_t)fminf(want, (float)sa.pmax);
     part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
     // The ragged lower bound keeps items of a few hundred tokens from paying
     // their fixed costs too often; with equal lengths every resident
@@ -1330,12 +1360,16 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
   // hold them at the upper partition bound.
   while (true) {
     const int P = sc.partition;
+    const DivU32 dv = div_setup((uint32_t)P);
+    int fq[E], fr[E];   // c / P and c % P
     int fs = 0, ps = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = tid * E + e;
-      fs += i < S ? c[e] / P : 0;
-      ps += i < S ? ((c[e] % P != 0 || c[e] == 0) ? 1 : 0) : 0;
+      fq[e] = (int)div_q(dv, (uint32_t)c[e]);
+      fr[e] = c[e] - fq[e] * P;
+      fs += i < S ? fq[e] : 0;
+      ps += i < S ? ((fr[e] != 0 || c[e] == 0) ? 1 : 0) : 0;
     }
     const int fi = wave_scan_i(fs), pi = wave_scan_i(ps);
     if (lane == kWave - 1) {
@@ -1369,16 +1403,20 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = tid * E + e;
-      const int r = c[e] % P;
+      const int r = fr[e];
       band[e] = -1;
       if (i < S) {
         ss.full_pre[i] = fo;
         ss.part_pre[i] = (uint16_t)po;
         ss.rem[i] = (uint16_t)r;
-        fo += c[e] / P;
+        fo += fq[e];
         if (r != 0 || c[e] == 0) {
           po += 1;
-          band[e] = (kShortBuckets - 1) - (int)((long long)r * kShortBuckets / P);
+          // floor(r * kShortBuckets / P) by comparisons (r < P <= 8192)
+          int b = kShortBuckets - 1;
+#pragma unroll
+          for (int k = 1; k < kShortBuckets; ++k) b -= (r * kShortBuckets >= k * P) ? 1 : 0;
+          band[e] = b;
           cnt += 1ull << (16 * band[e]);
         }
       }
@@ -1444,19 +1482,25 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
   const int S = sh.num_seqs, hkv = sh.num_kv_heads, nchunk = sh.nchunk;
   const int P = __builtin_amdgcn_readfirstlane(sc.partition);
   const int n_full = __builtin_amdgcn_readfirstlane(sc.n_full);
-  // Claim class of this work-group (its XCD under the usual round-robin
-  // dispatch): rows r with r % 8 == cls, each followed by its kv heads and
-  // head chunks, so every XCD reads every kv head and the chunks of one
-  // (row, kv head) run at about the same time on one XCD and share its L2.
+  // Claim classes.  Eight, one per XCD under the usual round-robin dispatch:
+  // rows r with r % 8 == cls, each followed by its kv heads and head chunks,
+  // so the chunks of one (row, kv head) run at about the same time on one XCD
+  // and share its L2.  Ragged lengths with one chunk per kv head (no two
+  // items read the same K/V rows) use one class over all work-groups, so
+  // the XCDs that start first take work from the ones that start late (same
+  // box: bench config 5 32/8 FP16 278.9 -> 274.2 us, INT8 163.7 -> 162.3;
+  // equal lengths measured 0.3-2.6% slower with one class and keep eight).
   const int n_rows = __builtin_amdgcn_readfirstlane(sc.n_rows);
   const int per_row = hkv * nchunk;
-  const int cls = blockIdx.x & 7;
-  const int groups_c = ((int)gridDim.x - cls + 7) >> 3;
-  const int items_c = (n_rows > cls ? (n_rows - cls + 7) >> 3 : 0) * per_row;
+  const int lg = (nchunk > 1 || sc.uniform) ? 3 : 0;   // log2 of the class count
+  const int ncls = 1 << lg;
+  const int cls = blockIdx.x & (ncls - 1);
+  const int groups_c = ((int)gridDim.x - cls + ncls - 1) >> lg;
+  const int items_c = (n_rows > cls ? (n_rows - cls + ncls - 1) >> lg : 0) * per_row;
   uint32_t* queue = sa.queue + cls * kSchedQueueStride;
   // Item indices are compared unsigned: whatever a claim counter holds, no
   // work-group leaves its class's item list.
-  int idx = blockIdx.x >> 3;   // index within the class: static first item
+  int idx = blockIdx.x >> lg;   // index within the class: static first item
   // With no more items than work-groups in the class (equal lengths give one
   // item per work-group) the static first items cover the class: no claims,
   // and the counter stays at zero.
@@ -1475,7 +1519,7 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
         old = __hip_atomic_fetch_add(queue + z, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     };
-    const int row = cls + 8 * (idx / per_row);
+    const int row = cls + ncls * (idx / per_row);
     const int sub = idx - (idx / per_row) * per_row;
     const int kvh = sub / nchunk, chunk = sub - (sub / nchunk) * nchunk;
     // Item fields are work-group uniform: keep them in scalar registers.
