@@ -368,6 +368,12 @@ struct DecodeWave {
   // the scales of 4 tokens and the others reach the lanes that need them by
   // quad DPP broadcasts.
   static constexpr bool W8 = I8 && D <= 128 && CT == 1;
+  // FP16 with head_dim > 128: the query operand is read from LDS at each QK
+  // (its KC * 4 registers would not fit beside the accumulators and the K/V
+  // rows in flight within 256 VGPRs; they spilled).  The work-group stages
+  // the tile once (stage_query), rows of QROW halves.
+  static constexpr bool QLDS = !I8 && D > 128;
+  static constexpr int QROW = D + 8;   // (row stride 16 B off a bank multiple)
 
   // Block ids of a lane's K rows and V rows (W8: one 16-token group each).
   struct Blocks {
@@ -390,9 +396,10 @@ struct DecodeWave {
   float m_run[CT], l_part[CT];
   f4_t acc[CT][NT];
   int e_cur;
-  // Query operand: lane (r, g) holds q[head r + 16 ct][32kk + 8g .. +7]; INT8:
-  // the K bias 1152 * sum(q) per head.
+  // Query operand: lane (r, g) holds q[head r + 16 ct][32kk + 8g .. +7]
+  // (QLDS: read from qs instead); INT8: the K bias 1152 * sum(q) per head.
   h8_t qreg[CT][KC];
+  const half_t* qs;
   float qbias[CT];
   // Loads of the chunk in flight.
   LVec kx[PAIRS][KC], ky[PAIRS][KC], vr[PAIRS][NT];
@@ -435,6 +442,12 @@ struct DecodeWave {
         qreg[ct][kk] = __builtin_bit_cast(h8_t, v);
       }
     }
+  }
+
+  // QLDS: the query operand of k-chunk kk from the staged tile.
+  __device__ __forceinline__ h8_t q_operand(int ct, int kk) const {
+    if constexpr (QLDS) return *reinterpret_cast<const h8_t*>(qs + r * QROW + 32 * kk + 8 * g);
+    else return qreg[ct][kk];
   }
 
   // INT8: the K bias of each head, once the query operand has arrived.
@@ -650,8 +663,9 @@ struct DecodeWave {
         }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-          sx[ct] = mfma16(ax, qreg[ct][kk], sx[ct]);
-          sy[ct] = mfma16(ay, qreg[ct][kk], sy[ct]);
+          const h8_t qo = q_operand(ct, kk);
+          sx[ct] = mfma16(ax, qo, sx[ct]);
+          sy[ct] = mfma16(ay, qo, sy[ct]);
         }
       }
 #pragma unroll
@@ -826,6 +840,47 @@ struct DecodeWave {
   }
 };
 
+// The query tile of one head chunk (q rows row0 .. row0 + gt - 1, zeros for
+// the tile's other rows) for waves that read their query operand from LDS
+// (DecodeWave::QLDS): every thread of the work-group loads 16-byte pieces
+// (load, issued before the context length is known) and stores them into
+// rows of D + 8 halves (store) over the wave-merge slots, which hold nothing
+// between a work item's start and its first wave-state store.
+template <int D, int NW>
+struct QueryStage {
+  static constexpr int QROW = D + 8;
+  static constexpr int PIECES = 16 * D / 8;
+  static constexpr int N = (PIECES + NW * kWave - 1) / (NW * kWave);   // pieces per thread
+  uint4 v[N];
+
+  __device__ __forceinline__ void load(const half_t* __restrict__ q, size_t row0, int gt, int tid) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int i = tid + k * NW * kWave;
+      const int row = i / (D / 8), cg = i % (D / 8);
+      v[k] = (i < PIECES && row < gt)
+                 ? *reinterpret_cast<const uint4*>(q + (row0 + row) * D + 8 * cg)
+                 : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  __device__ __forceinline__ void store(half_t* qs, int tid) const {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int i = tid + k * NW * kWave;
+      if (i < PIECES) *reinterpret_cast<uint4*>(qs + (i / (D / 8)) * QROW + 8 * (i % (D / 8))) = v[k];
+    }
+  }
+};
+
+// Where QLDS waves find the staged query tile: the start of the wave-merge slots.
+template <typename Smem>
+__device__ __forceinline__ half_t* query_stage_lds(Smem& sm) {
+  static_assert(16 * (sizeof(sm.a[0][0]) / sizeof(float) + 8) * sizeof(half_t) <= sizeof(sm.a),
+                "the query tile fits in the wave-merge slots");
+  return reinterpret_cast<half_t*>(&sm.a[0][0][0]);
+}
+
 // The NW wave states of item (head hh of a column tile, dims 4c .. 4c + 3) in
 // LDS, merged: accumulator relative to the max, the max and the sum.
 template <int D, int NW, typename Smem>
@@ -943,7 +998,13 @@ __device__ __forceinline__ void decode_split(
     const int i = tid + k * NW * kWave;
     staged[k] = i < nstage ? btrow[b_first + i] : 0;
   }
-  dw.load_q(q, (size_t)seq * sh.num_heads + head0, gt);
+  [[maybe_unused]] QueryStage<D, NW> qst;
+  if constexpr (Wave::QLDS) {
+    qst.load(q, (size_t)seq * sh.num_heads + head0, gt, tid);
+    dw.qs = query_stage_lds(sm);
+  } else {
+    dw.load_q(q, (size_t)seq * sh.num_heads + head0, gt);
+  }
   dw.compute_qbias();
 
   if (!resolve(wk.ctx, wk.ns)) return;   // work-group uniform, before any barrier
@@ -951,6 +1012,10 @@ __device__ __forceinline__ void decode_split(
   const int t_end = min(wk.ctx, t_begin + wk.partition);
   const int n_it = t_end > t_begin ? (t_end - t_begin + IT - 1) / IT : 0;
   const int nblk = t_end > t_begin ? min(((t_end - 1) >> bsl) - b_first + 1, nstage) : 0;
+  if constexpr (Wave::QLDS) {
+    lds_barrier();   // a previous work item's wave merge has read the slots
+    qst.store(query_stage_lds(sm), tid);
+  }
 #pragma unroll
   for (int k = 0; k < kStageRegs; ++k) {
     const int i = tid + k * NW * kWave;
@@ -1032,6 +1097,7 @@ __device__ __forceinline__ void decode_split(
   for (int ct = 0; ct < CT; ++ct) {
     const int nh = min(16, gt - 16 * ct);   // query heads of this tile
     if (ct > 0) __syncthreads();            // the previous tile's merge has read its slots
+    else if constexpr (Wave::QLDS) lds_barrier();   // every wave's last QK has read the query tile
     dw.store_state(sm, w, ct, nh);
     __syncthreads();
     merge_wave_states<D, NW, FUSED>(sm, ct, nh, tid, final_here, out, out_base, racc, rml);
@@ -1748,7 +1814,16 @@ decode_stream_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
     const bool whole = seg_lo == sg.end - sg.nch && seg_hi == sg.end;
     const int kvh = kv_head(sg), chunk = sg.u - kvh * sh.nchunk;
     const int head0 = kvh * sh.group + chunk * gt;
-    dw.load_q(q, (size_t)sg.s * sh.num_heads + head0, gt);
+    if constexpr (Wave::QLDS) {
+      QueryStage<D, NW> qst;
+      qst.load(q, (size_t)sg.s * sh.num_heads + head0, gt, tid);
+      lds_barrier();   // the previous part's wave merge has read the slots
+      qst.store(query_stage_lds(sm), tid);
+      lds_barrier();
+      dw.qs = query_stage_lds(sm);
+    } else {
+      dw.load_q(q, (size_t)sg.s * sh.num_heads + head0, gt);
+    }
     dw.compute_qbias();
     dw.reset();
     while (have && cur.x < seg_hi) {

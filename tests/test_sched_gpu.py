@@ -78,6 +78,21 @@ def test_ragged_fp16(mode, variant, heads):
 
 
 @pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
+@pytest.mark.parametrize("variant", ["warp", "splitk"])
+@pytest.mark.parametrize("partition", [0, 64])
+def test_ragged_fp16_head_dim_256(mode, variant, partition):
+    """FP16 at head_dim 256 reads its query operand from a tile staged in LDS
+    over the wave-merge slots.  Many work items per work-group (the schedule,
+    small forced partitions) and many stream parts per work-group (the stream
+    partition) check that no item's query tile meets another item's merge."""
+    _mode(mode)
+    lens = ragged_lens(41, seed=7)
+    c = fp16_case(len(lens), lens, 8, 2, head_dim=256, seed=21)
+    assert_close(run(c, variant, partition=partition), oracle_fp16(c),
+                 what=f"mode {mode} {variant} partition {partition}")
+
+
+@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp_int8", "splitk_int8"])
 @pytest.mark.parametrize("heads", [(16, 8), (32, 1)])
 def test_ragged_int8(mode, variant, heads):
