@@ -97,3 +97,37 @@ def test_int8_bridges_track_fp16(model):
     assert err["int8_per_token"].max() < 0.5
     assert err["int8_per_token"].mean() < 0.1
     assert err["int8_per_token"].mean() <= err["int8_per_tensor"].mean() * 1.1 + 1e-3
+
+
+@pytest.fixture(scope="module")
+def model_bf16():
+    from pa_int8 import qwen_bridge as br
+
+    br.register()
+    return tiny_qwen(dtype=torch.bfloat16, device="cuda")
+
+
+def test_bf16_model_through_the_bridge(model_bf16):
+    """The reference's runner loads the model in bfloat16
+    (benchmarks/int8_bridge/run_bridge.py:99).  The bridge then hands the
+    kernel an fp16 copy of the query; the fp16 cache converts the bf16 K/V
+    (exactly), and the INT8 caches quantize them directly, as
+    quantize_per_token does on bf16.  The fp16 cache must match the dense fp32
+    reference on the same model; the INT8 caches must track the fp16 cache as
+    they do on an fp16 model."""
+    prompt, cont = _tokens(48, 21), _tokens(16, 22)
+    want = _reference_logprobs(model_bf16, prompt, cont)
+    fp, cache = _bridge_logprobs(model_bf16, prompt, cont, "fp16")
+    err = np.abs(fp - want)
+    print(f"bf16 model, fp16 cache: max |dlogp| vs dense fp32 {err.max():.2e}, "
+          f"mean {err.mean():.2e}")
+    assert cache.lengths == [48 + 16 - 1] * model_bf16.config.num_hidden_layers
+    assert err.max() < 2 * LOGP_MAX
+    for variant in ("int8_per_token", "int8_per_tensor"):
+        lp, cache = _bridge_logprobs(model_bf16, prompt, cont, variant)
+        assert cache.k_scales.dtype == torch.float32
+        e = np.abs(lp - fp)
+        print(f"bf16 model, {variant}: max |dlogp| vs fp16 cache {e.max():.3e}, "
+              f"mean {e.mean():.3e}")
+        assert e.max() < 0.5
+        assert e.mean() < 0.1
