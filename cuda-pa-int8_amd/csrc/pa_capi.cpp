@@ -48,7 +48,10 @@ constexpr int kRefTile = 128;        // reference TILE (paged_attention_v3_warp.
 // round trips, larger ones leave CUs idle.
 constexpr int kTargetWaves = 2048;   // waves one decode launch aims for (256 CUs x 8)
 constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
-constexpr int kSchedMinPartition = 1024;   // per 4 waves, in-kernel schedule
+// Shortest item of the in-kernel schedule on ragged lengths, in tokens at
+// head_dim <= 128 (half that above, where a token holds twice the bytes),
+// whatever the group size.
+constexpr int kSchedMinItemTokens = 2048;
 // Test and tuning overrides (pa_mi355x_tuning.h), per calling thread.
 thread_local int g_waves_override = 0;
 thread_local int g_schedule_mode = 0;   // 0 auto, 1 grid, 2 in-kernel schedule
@@ -207,9 +210,11 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
     if (partition_tokens > 0) {
       p.pmin = p.pmax = p.pmin_uniform = p.partition;
     } else {
-      // Items below ~1 MB of FP16 K/V pay their fixed start-up and merge
-      // costs too often (partition sweeps of the ragged mix on MI355X).
-      p.pmin = kSchedMinPartition * p.waves / 4;
+      // Shorter items pay their fixed start-up and merge costs too often
+      // (forced-partition sweeps of bench config 5 on MI355X, same box: 2048
+      // against 1024 tokens, INT8 in 4-wave groups, 32/8 161.9 -> 156.2 us,
+      // MQA 32/1 41.2 -> 39.7 us; FP16 in 8-wave groups was already at 2048).
+      p.pmin = head_dim <= 128 ? kSchedMinItemTokens : kSchedMinItemTokens / 2;
       // Equal lengths: one item per resident work-group, down to the grid
       // plan's bound (config 2 would otherwise run on half the work-groups).
       p.pmin_uniform = kMinPartition * p.waves / 4;
