@@ -164,6 +164,16 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // INT8 +0.5-1.3%; FP16 with one chunk gains nothing (ragged +1.4%).
   if (ov == 0 && !is_fused(kind) && (!is_f16(kind) || p.nchunk > 1)) p.waves = 4;
   if (ov == 0 && p.stream) p.waves = 4;
+  // The single-launch INT8 kind in its 16-byte-load form (one 16-head
+  // tile): one 4-wave work-group per CU, with the partition an 8-wave plan
+  // would take, so each SIMD serves one wave's chunk math.  Same box,
+  // alternating processes: config 3 48.2 -> 47.6 us, config 2 INT8 16.9 ->
+  // 16.6, config 4 32k 91.6 -> 90.3 (64k +0.6%).  The 32-head form (8-byte
+  // loads, 32 tokens per iteration) needs its 8 waves: MQA 32/1 on 8 x 32k
+  // 33.0 -> 40.6 us with 4.
+  const bool int8_quad = ov == 0 && kind == PA_DECODE_WARP_I8 && head_dim <= 128 &&
+                         p.head_tile <= 16;
+  if (int8_quad) p.waves = 4;
   if (head_dim > 128) p.waves = 4;     // LDS of the 8-wave merge exceeds 64 KB
   long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
   if (ctx < 1) ctx = 1;
@@ -174,7 +184,7 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
     part = std::min<long long>(partition_tokens, hi);
   } else {
     const long long units = std::max(1, p.units);
-    const long long groups = kTargetWaves / p.waves;
+    const long long groups = kTargetWaves / (int8_quad ? 8 : p.waves);
     const long long lo = (long long)kMinPartition * p.waves / 4;
     part = (ctx * units + groups - 1) / groups;
     part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
