@@ -164,19 +164,24 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // INT8 +0.5-1.3%; FP16 with one chunk gains nothing (ragged +1.4%).
   if (ov == 0 && !is_fused(kind) && (!is_f16(kind) || p.nchunk > 1)) p.waves = 4;
   if (ov == 0 && p.stream) p.waves = 4;
-  // The single-launch INT8 kind in its 16-byte-load form (one 16-head
-  // tile): one 4-wave work-group per CU, with the partition an 8-wave plan
-  // would take, so each SIMD serves one wave's chunk math.  Same box,
-  // alternating processes: config 3 48.2 -> 47.6 us, config 2 INT8 16.9 ->
-  // 16.6, config 4 32k 91.6 -> 90.3 (64k +0.6%).  The 32-head form (8-byte
-  // loads, 32 tokens per iteration) needs its 8 waves: MQA 32/1 on 8 x 32k
-  // 33.0 -> 40.6 us with 4.
-  const bool int8_quad = ov == 0 && kind == PA_DECODE_WARP_I8 && head_dim <= 128 &&
-                         p.head_tile <= 16;
-  if (int8_quad) p.waves = 4;
-  if (head_dim > 128) p.waves = 4;     // LDS of the 8-wave merge exceeds 64 KB
   long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
   if (ctx < 1) ctx = 1;
+  // K/V bytes of the launch if every sequence held `ctx` tokens.
+  const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
+                             (is_f16(kind) ? 2 : 1);
+  // Single-launch kinds with one 16-head column tile that read enough to be
+  // bandwidth-bound: one 4-wave work-group per CU, with the partition an
+  // 8-wave plan would take, so each SIMD serves one wave's chunk math.  Same
+  // box, alternating processes: INT8 config 3 48.2 -> 47.6 us, config 2 16.9
+  // -> 16.6, config 4 32k 91.6 -> 90.3 (64k +0.6%); FP16 config 3 85.8 ->
+  // 83.9, config 2 25.6 -> 25.3, the reference's GQA shapes 0.8-1.4%.  The
+  // 32-head form (8-byte INT8 loads, 32 tokens per iteration) keeps 8 waves
+  // (INT8 MQA 32/1 on 8 x 32k 33.0 -> 40.6 us with 4), and so do launches
+  // below kNtMinBytes, which are latency-bound (config 1 4.8 -> 5.7 us with 4).
+  const bool quad = ov == 0 && is_fused(kind) && head_dim <= 128 && p.head_tile <= 16 &&
+                    kv_bytes > kNtMinBytes;
+  if (quad) p.waves = 4;
+  if (head_dim > 128) p.waves = 4;     // LDS of the 8-wave merge exceeds 64 KB
   long long part;
   // Caps the serial work of a work-group and keeps a split's block ids in LDS.
   const long long hi = (long long)pa::max_partition_per_4_waves(head_dim) * p.waves / 4;
@@ -184,7 +189,7 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
     part = std::min<long long>(partition_tokens, hi);
   } else {
     const long long units = std::max(1, p.units);
-    const long long groups = kTargetWaves / (int8_quad ? 8 : p.waves);
+    const long long groups = kTargetWaves / (quad ? 8 : p.waves);
     const long long lo = (long long)kMinPartition * p.waves / 4;
     part = (ctx * units + groups - 1) / groups;
     part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
@@ -205,8 +210,6 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // latency-bound and its tiles may still sit in the 256 MB Infinity Cache
   // from an earlier call, which plain loads can hit (config 1: 4.6 us plain,
   // 6.0 us non-temporal); non-temporal loads start at 32 MB.
-  const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
-                             (is_f16(kind) ? 2 : 1);
   const int lm = g_load_mode;
   p.nt_loads = lm == 2 || (lm == 0 && p.nchunk == 1 && kv_bytes > kNtMinBytes);
 
