@@ -27,13 +27,17 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // Row-local DPP move (all rows and banks enabled, every source lane valid).
+// No lane keeps the destination's old value, so none is supplied (an
+// explicit one, update_dpp's first operand, costs a move per call).  Call it
+// with every lane active: a lane whose source lane is inactive would read an
+// undefined value.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
-  return bitsf((uint32_t)__builtin_amdgcn_update_dpp(0, (int)fbits(v), CTRL, 0xF, 0xF, false));
+  return bitsf((uint32_t)__builtin_amdgcn_mov_dpp((int)fbits(v), CTRL, 0xF, 0xF, false));
 }
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_mov_u(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
 }
 
 // DPP controls used below.
