@@ -124,16 +124,6 @@ __device__ __forceinline__ h8_t i8x8_biased(uint2 w) {
   i8x4_to_biased_h2(w.y, d[2], d[3]);
   return __builtin_bit_cast(h8_t, d);
 }
-// 8 int8 values -> the same values in fp16 (exact).
-__device__ __forceinline__ h8_t i8x8_exact(uint2 w) {
-  uint32_t d[4];
-  i8x4_to_biased_h2(w.x, d[0], d[1]);
-  i8x4_to_biased_h2(w.y, d[2], d[3]);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) d[k] = unbias_h2(d[k]);
-  return __builtin_bit_cast(h8_t, d);
-}
-
 // Zero the fp16 elements e >= n of an 8-element row (tokens past the end may
 // hold NaN bits, and 0 * NaN would poison the PV product).
 __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
@@ -689,8 +679,10 @@ struct DecodeWave {
   __device__ __forceinline__ void softmax_pv(float (&s)[CT][PAIRS][8], bool need_mask, W8Buf& B,
                                              float c) {
     // W8: this lane's 4 scales; token 16g + 8p + j of the lane's row is held
-    // by quad position 2p + (j >> 2), element j & 3.
-    float ksa[4] = {B.ks4.x, B.ks4.y, B.ks4.z, B.ks4.w};
+    // by quad position 2p + (j >> 2), element j & 3.  The K scales carry the
+    // softmax scale c before they are broadcast (the same products, 4 instead
+    // of 16 multiplies).
+    float ksa[4] = {B.ks4.x * c, B.ks4.y * c, B.ks4.z * c, B.ks4.w * c};
     float vsa[4] = {B.vs4.x, B.vs4.y, B.vs4.z, B.vs4.w};
     auto nval = [&](int p) {
       if constexpr (W8) return B.nvalid[p];
@@ -708,7 +700,7 @@ struct DecodeWave {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float ksj = quad_bcast(ksa[j & 3], 2 * p + (j >> 2));
-          s[0][p][j] = (s[0][p][j] - qbias[0]) * (ksj * c);
+          s[0][p][j] = (s[0][p][j] - qbias[0]) * ksj;
         }
     } else {
 #pragma unroll
@@ -778,6 +770,13 @@ struct DecodeWave {
     } else {
       wsc = 16384.f;
     }
+    // W8: the V scales carry the weight scale 2^e before they are broadcast
+    // (exact: a power of two; weights too small for the product to stay
+    // normal round to an fp16 zero either way).
+    if constexpr (W8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vsa[i] *= wsc;
+    }
     h8_t pb[CT][PAIRS];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -789,7 +788,7 @@ struct DecodeWave {
           const float pj = exp2f_fast(s[ct][p][j] - m_use[ct]);
           lsum += pj;
           float wj;
-          if constexpr (W8) wj = pj * quad_bcast(vsa[j & 3], 2 * p + (j >> 2)) * wsc;
+          if constexpr (W8) wj = pj * quad_bcast(vsa[j & 3], 2 * p + (j >> 2));
           else if constexpr (I8) wj = pj * vsv[p][j] * wsc;
           else wj = pj * wsc;
           pb[ct][p][j] = (half_t)wj;
@@ -802,16 +801,31 @@ struct DecodeWave {
       }
     }
 
-    // ---- PV: each converted V operand feeds every column tile
+    // ---- PV: each converted V operand feeds every column tile.  INT8: V
+    // enters as 1152 + v (its conversion without an unbias step per
+    // element); ws sums each head's weights of this chunk (an MFMA with a ones
+    // operand: every element of lane (r, g) holds head r's sum), and the
+    // chunk's 1152 * sum(w) comes off after its products, so the accumulator
+    // carries no bias from one chunk to the next.
+    [[maybe_unused]] f4_t ws[CT];
+    if constexpr (I8) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) ws[ct] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int p = 0; p < PAIRS; ++p) {
+      if constexpr (I8) {
+        const h8_t ones = {1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16, 1.f16};
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) ws[ct] = mfma16(ones, pb[ct][p], ws[ct]);
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         h8_t av;
         if constexpr (W8) {
-          av = i8x8_exact(p == 0 ? make_uint2(vw[t].x, vw[t].y) : make_uint2(vw[t].z, vw[t].w));
+          av = i8x8_biased(p == 0 ? make_uint2(vw[t].x, vw[t].y) : make_uint2(vw[t].z, vw[t].w));
         } else if constexpr (I8) {
-          av = i8x8_exact(vr[p][t]);
+          av = i8x8_biased(vr[p][t]);
         } else {
           uint4 v = vr[p][t];
           if (need_mask) v = keep_first(v, nval(p));
@@ -819,6 +833,14 @@ struct DecodeWave {
         }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[ct][t] = mfma16(av, pb[ct][p], acc[ct][t]);
+      }
+    }
+    if constexpr (I8) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const float b = 1152.f * ws[ct][0];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[ct][t] -= b;
       }
     }
   }

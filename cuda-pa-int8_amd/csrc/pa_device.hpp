@@ -103,13 +103,6 @@ __device__ __forceinline__ void i8x4_to_biased_h2(uint32_t w, uint32_t& lo, uint
   hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
 }
 
-// The same conversion with the 1152 bias removed (exact: integers < 2048).
-__device__ __forceinline__ uint32_t unbias_h2(uint32_t v) {
-  half2_t h = __builtin_bit_cast(half2_t, v);
-  h = h - (half2_t){(_Float16)1152.0f, (_Float16)1152.0f};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
 // A load of data that is read once (cache tiles, inputs of the write
 // kernels): the non-temporal hint keeps it from being retained in the caches.
 // On MI355X it raised the decode kernels' streaming rate from about 5.9 to
