@@ -98,8 +98,8 @@ pa_status_t pa_check_context_lens(const int32_t* host_context_lens, int32_t num_
  * actual lengths; a forced partition_tokens is used as given by both.)  `max_context_len` <= 0
  * means "use max_blocks_per_seq * block_size".  `partition_tokens` > 0
  * forces the partition size (rounded up to a multiple of 64 and capped at
- * 1024 tokens per wave of the work-group: 8192 for head_dim <= 128, 4096
- * for head_dim 256). */
+ * 2048 tokens per wave of the work-group for head_dim <= 128, 8192 with 4
+ * waves and 16384 with 8, and at 1024 per wave, 4096, for head_dim 256). */
 pa_status_t pa_decode_plan(pa_decode_kind_t kind, int32_t num_seqs, int32_t num_heads,
                            int32_t head_dim, int32_t num_kv_heads, int32_t block_size,
                            int32_t max_blocks_per_seq, int32_t max_context_len,
