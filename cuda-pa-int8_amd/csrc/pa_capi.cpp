@@ -171,7 +171,8 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
                              (is_f16(kind) ? 2 : 1);
   // Single-launch kinds with one 16-head column tile that read enough to be
   // bandwidth-bound: one 4-wave work-group per CU, with the partition an
-  // 8-wave plan would take, so each SIMD serves one wave's chunk math.  Same
+  // 8-wave plan would take (up to the 4-wave cap of 8192 tokens, which keeps
+  // a split's block ids in LDS), so each SIMD serves one wave's chunk math.  Same
   // box, alternating processes: INT8 config 3 48.2 -> 47.6 us, config 2 16.9
   // -> 16.6, config 4 32k 91.6 -> 90.3 (64k +0.6%); FP16 config 3 85.8 ->
   // 83.9, config 2 25.6 -> 25.3, the reference's GQA shapes 0.8-1.4%.  The
@@ -189,8 +190,9 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
     part = std::min<long long>(partition_tokens, hi);
   } else {
     const long long units = std::max(1, p.units);
-    const long long groups = kTargetWaves / (quad ? 8 : p.waves);
-    const long long lo = (long long)kMinPartition * p.waves / 4;
+    const int plan_waves = quad ? 8 : p.waves;   // the group size the split count assumes
+    const long long groups = kTargetWaves / plan_waves;
+    const long long lo = (long long)kMinPartition * plan_waves / 4;
     part = (ctx * units + groups - 1) / groups;
     part = (part + kMinPartition - 1) / kMinPartition * kMinPartition;
     part = std::min(std::max(part, lo), hi);
