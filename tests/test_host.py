@@ -152,6 +152,30 @@ def test_probe_host_checks(built):
     assert lib.pa_probe_read_write(16, 1 << 34, 16, 64, None) == 2     # output past 4 GiB
 
 
+def test_single_launch_group_sizes(lib):
+    """The single-launch kinds run one 4-wave work-group per CU (256 of them
+    at configs 2 and 3) with a 16-head tile on launches over 32 MB; the
+    32-head tile (MQA) and small, latency-bound launches keep 8 waves."""
+    info = (ctypes.c_int32 * 8)()
+
+    def plan(kind, s, h, d, hkv, ctx):
+        assert lib.pa_decode_plan_detail(kind, s, h, d, hkv, 16, (ctx + 15) // 16, ctx, 0, info,
+                                         8) == 0
+        return dict(partition=info[0], splits=info[1], waves=info[2], tile=info[3])
+
+    for kind in (0, 2):                                   # warp, warp_int8
+        p = plan(kind, 32, 12, 128, 2, 4096)              # config 2: 64 units x 4 splits
+        assert (p["waves"], p["partition"], p["splits"]) == (4, 1024, 4), (kind, p)
+        p = plan(kind, 64, 12, 128, 2, 8192)              # config 3: 128 units x 2 splits
+        assert (p["waves"], p["partition"], p["splits"]) == (4, 4096, 2), (kind, p)
+        p = plan(kind, 8, 32, 128, 1, 32768)              # MQA: one 32-head tile per kv head
+        assert p["tile"] == 32 and p["waves"] == 8, (kind, p)
+    p = plan(0, 4, 8, 64, 8, 512)                         # config 1: tiny, latency-bound
+    assert p["waves"] == 8, p
+    p = plan(0, 1, 8, 128, 8, 4096)                       # 16.8 MB, below the 32 MB threshold
+    assert p["waves"] == 8, p
+
+
 def test_waves_override_hook(lib):
     assert lib.pa_decode_set_waves_per_group(3) == 2
     for w in (4, 8, 0):
