@@ -360,6 +360,28 @@ def run_decode_cfg(torch, name, lens, h, hkv, d, variant, steps, warmup, seed=0,
     return res
 
 
+def probe_quant_write(torch, k, v, slots, dests, steps, warmup, replays=3):
+    """Time of the write kernel's address-stream probe (libpa_bench_probe.so):
+    the same launch, loads and stores over the same inputs, slots and
+    destination caches, with the quantization replaced by a byte pick (it
+    overwrites the caches)."""
+    from pa_int8._loader import probe_capi
+
+    lib = probe_capi()
+    T, hkv, _ = k.shape
+    fns = []
+    for kc, vc, ks, vs in dests:
+        def fn(kc=kc, vc=vc, ks=ks, vs=vs):
+            st = lib.pa_probe_quant_write(
+                k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                slots.data_ptr(), T, hkv, kc.data_ptr(), vc.data_ptr(), ks.data_ptr(),
+                vs.data_ptr(), kc.shape[0], kc.shape[3], torch.cuda.current_stream().cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"pa_probe_quant_write: status {st}")
+        fns.append(fn)
+    return time_steps(torch, fns, steps, warmup, replays)
+
+
 def run_quant_write(torch, steps, warmup, seed=0):
     import pa_int8
     from pa_int8 import metrics
@@ -418,6 +440,16 @@ def run_quant_write(torch, steps, warmup, seed=0):
                gate="4096 sampled tokens: int8 bytes and scale bits equal torch's "
                     "quantize_per_token on the device")
     log(f"[bench] cfg3w quant_write: {res['us']} us, {res['gbs']} GB/s")
+    # after the gate and the timing: the probe overwrites the caches
+    pms = probe_quant_write(torch, k, v, slots, dests, steps, warmup)
+    res["write_stream_probe"] = dict(
+        us=round(pms * 1e3, 2), gbs=round(nbytes / (pms * 1e-3) / 1e9, 1),
+        write_over_probe=round(ms / pms, 3),
+        note="the write kernel's own launch, loads and stores with the quantization replaced by "
+             "a byte pick (pa_probe_quant_write): its address stream alone")
+    log(f"[bench] cfg3w quant_write address-stream probe: {res['write_stream_probe']['us']} us "
+        f"({res['write_stream_probe']['gbs']} GB/s; write / probe = "
+        f"{res['write_stream_probe']['write_over_probe']})")
     del k, v, dests
     torch.cuda.empty_cache()
     return res

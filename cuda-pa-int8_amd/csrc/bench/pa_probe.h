@@ -52,6 +52,19 @@ pa_status_t pa_probe_decode_stream(int32_t int8_kv, const void* q, const void* k
                                    int32_t waves, int32_t load_flags, uint32_t* sink,
                                    pa_stream_t stream);
 
+/* pa_probe_quant_write runs the INT8 write kernel's launch (fp16 key / value,
+ * per-token scales, head_dim 128) with the same loads and stores but no
+ * quantization: each element's high byte is stored, and a scale of 1.  Its
+ * time is the memory system's for the write kernel's address stream.  The
+ * arguments are those of pa_reshape_and_cache_int8 (x = 8); the caches are
+ * overwritten. */
+pa_status_t pa_probe_quant_write(const void* key, const void* value, int64_t key_token_stride,
+                                 int64_t key_head_stride, int64_t value_token_stride,
+                                 int64_t value_head_stride, const int64_t* slot_mapping,
+                                 int32_t num_tokens, int32_t num_kv_heads, void* k_cache,
+                                 void* v_cache, float* k_scales, float* v_scales,
+                                 int32_t num_blocks, int32_t block_size, pa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

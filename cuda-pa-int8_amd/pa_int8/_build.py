@@ -44,7 +44,7 @@ HIP_SOURCES = [
     "pa_noalloc.hip",
 ]
 HOST_SOURCES = ["pa_capi.cpp"]
-PROBE_SOURCES = ["bench/pa_probe.hip", "bench/pa_probe_decode.hip"]
+PROBE_SOURCES = ["bench/pa_probe.hip", "bench/pa_probe_decode.hip", "bench/pa_probe_write.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -120,6 +120,8 @@ PROBE_PROTOTYPES = {
     "pa_probe_read_write": (ctypes.c_int, [_p, _sz, _p, _i32, _p]),
     "pa_probe_decode_stream": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
                                               _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+    "pa_probe_quant_write": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i64, _p, _i32, _i32, _p, _p,
+                                            _p, _p, _i32, _i32, _p]),
 }
 
 

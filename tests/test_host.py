@@ -150,6 +150,13 @@ def test_probe_host_checks(built):
     assert lib.pa_probe_read_write(None, 1 << 20, 16, 64, None) == 1
     assert lib.pa_probe_read_write(16, 1 << 20, 16, 0, None) == 2
     assert lib.pa_probe_read_write(16, 1 << 34, 16, 64, None) == 2     # output past 4 GiB
+    # the write-stream probe: the write op's argument rules, checked on the host
+    args = [16, 16, 512, 256, 512, 256, 16, 64, 2, 16, 16, 16, 16, 100]
+    assert lib.pa_probe_quant_write(None, *args[1:], 16, None) == 1
+    for bs in (8, 24, 256):
+        assert lib.pa_probe_quant_write(*args, bs, None) == 3
+    assert lib.pa_probe_quant_write(16, 16, 512, 256, 512, 260, *args[6:], 16, None) == 2
+    assert lib.pa_probe_quant_write(24, *args[1:], 16, None) == 2      # unaligned key
 
 
 def test_single_launch_group_sizes(lib):
