@@ -259,3 +259,48 @@ def test_quant_write_full_size_then_decode():
     ratio = assert_close(out[:4].float().cpu().numpy(), want, what="decode after write")
     record_headroom("cfg3", "warp_int8 64 x 8192 12/2 over the kernel-written cache", ratio,
                     variant="warp_int8", seqs_checked=4)
+
+
+@pytest.mark.parametrize("block_size", [16, 32])
+@pytest.mark.parametrize("pattern", ["prefill", "scattered", "padding"])
+def test_write_stream_probe_stores_where_the_kernel_does(block_size, pattern):
+    """The benchmark's write-stream probe (pa_probe_quant_write, the write
+    kernel's template in its PROBE form) stores each element's high byte and a
+    scale of 1 at exactly the cache positions the write op fills, and leaves
+    every other byte alone: its address stream is the kernel's."""
+    from pa_int8 import _loader
+
+    lib = _loader.probe_capi()
+    rng = np.random.default_rng(block_size + len(pattern))
+    T, hkv, d, bs = 80, 2, 128, block_size
+    k, v = make_kv(T, hkv, d, rng)
+    nb = (T + bs - 1) // bs * 2 + 3
+    slots = slots_for(pattern, T, nb, bs, rng)
+    kc = rng.integers(-128, 128, size=(nb, hkv, d // 8, bs, 8)).astype(np.int8)
+    vc = rng.integers(-128, 128, size=(nb, hkv, d, bs)).astype(np.int8)
+    ks = rng.standard_normal((nb, hkv, bs)).astype(np.float32)
+    vs = rng.standard_normal((nb, hkv, bs)).astype(np.float32)
+    want = [a.copy() for a in (kc, vc, ks, vs)]
+    hi = lambda x: (x.view(np.uint16) >> 8).astype(np.uint8).view(np.int8)
+    for t, s in enumerate(slots):
+        if not 0 <= s < nb * bs:
+            continue
+        blk, off = s // bs, s % bs
+        want[0][blk, :, :, off, :] = hi(k[t]).reshape(hkv, d // 8, 8)
+        want[1][blk, :, :, off] = hi(v[t])
+        want[2][blk, :, off] = 1.0
+        want[3][blk, :, off] = 1.0
+    tk, tv, ts = _t(k), _t(v), _t(slots)
+    g = [_t(a) for a in (kc, vc, ks, vs)]
+    st = lib.pa_probe_quant_write(tk.data_ptr(), tv.data_ptr(), tk.stride(0), tk.stride(1),
+                                  tv.stride(0), tv.stride(1), ts.data_ptr(), T, hkv,
+                                  g[0].data_ptr(), g[1].data_ptr(), g[2].data_ptr(),
+                                  g[3].data_ptr(), nb, bs, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    for name, got, exp in zip(("k_cache", "v_cache", "k_scales", "v_scales"), g, want):
+        got = got.cpu().numpy()
+        gb = got.view(np.uint8) if got.dtype == np.int8 else got.view(np.uint32)
+        eb = exp.view(np.uint8) if exp.dtype == np.int8 else exp.view(np.uint32)
+        bad = np.argwhere(gb != eb)
+        assert bad.size == 0, f"{name}: {len(bad)} mismatches, first at {bad[0].tolist()}"
