@@ -58,7 +58,7 @@ thread_local int g_schedule_mode = 0;   // 0 auto, 1 grid, 2 in-kernel schedule
 thread_local int g_load_mode = 0;       // 0 auto, 1 plain, 2 non-temporal cache-tile loads
 thread_local int g_head_tile_cap = 0;   // 0 auto, else the most query heads per work-group
 constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
-constexpr int kKntMinPartition = 4096;          // non-temporal K rows from this split size
+constexpr int kKntMinPartition = 1024;          // non-temporal K rows from this split size
 // Upper bound on resident decode work-groups used to size the partial
 // buffers of the in-kernel schedule (256 CUs x 2 groups on MI355X).
 constexpr int kSchedGroupsBound = 1024;
@@ -217,8 +217,9 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
 
   // K rows non-temporal as well: FP16 grid launches whose splits hold at least
   // kKntMinPartition tokens (same box, caches rotated over 4x the Infinity
-  // Cache: config 3 FP16 89.6 -> 86.4 us; config 2's 1024-token splits and
-  // INT8 measured faster with plain K).
+  // Cache: config 3 FP16 89.6 -> 86.4 us; with one 4-wave group per CU,
+  // config 2's 1024-token splits 25.38 -> 25.22 us and the reference's GQA
+  // shapes 0.4-1.4%; INT8 measured faster with plain K).
   p.k_nt = p.nt_loads && is_f16(kind) && !p.sched && !p.stream &&
            p.partition >= kKntMinPartition;
   if (p.sched) {

@@ -97,8 +97,8 @@ __device__ __forceinline__ float head_sum(float v) {
 // next (the two token halves of a row group), and non-temporal K lines can
 // leave the L2 in between (INT8 config 3 fetched 7% more), so K rows load
 // plain except under KNT, which the planner sets for FP16 grid launches with
-// long splits (>= 4096 tokens), where non-temporal K measured faster
-// (config 3 FP16 3.6%; plain K stays ahead for INT8, ragged batches and
+// splits of >= 1024 tokens, where non-temporal K measured faster (config 3
+// FP16 3.6%, config 2 0.6%; plain K stays ahead for INT8, ragged batches and
 // shorter splits).
 template <typename T, bool NTL>
 __device__ __forceinline__ T load_tile(const void* p) {

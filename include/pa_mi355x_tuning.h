@@ -40,7 +40,7 @@ pa_status_t pa_decode_set_schedule(int32_t mode);
 pa_status_t pa_decode_set_max_head_tile(int32_t heads);
 
 /* Cache hint of the V-row loads (K rows load plain, except in FP16 grid
- * launches whose splits hold at least 4096 tokens, which follow V).
+ * launches whose splits hold at least 1024 tokens, which follow V).
  * 0 = automatic: non-temporal when each kv head's tiles are read by one
  * work-group and the call reads more than 32 MB of K/V, plain otherwise;
  * 1 = plain; 2 = non-temporal. */

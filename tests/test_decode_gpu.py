@@ -548,7 +548,7 @@ def test_graph_replay_matches_eager(variant):
 @pytest.mark.parametrize("policy", [0, 1, 2])
 def test_load_policies_agree(head_dim, policy):
     """Every cache-load hint gives the oracle's result: plain (1), non-temporal
-    V (2; FP16 grid launches with splits of >= 4096 tokens then load K
+    V (2; FP16 grid launches with splits of >= 1024 tokens then load K
     non-temporally too) and automatic (0), on the grid and the scheduled forms,
     with two splits of 4096 tokens per sequence."""
     import pa_int8
