@@ -248,12 +248,13 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
 }
 
 // Counters (zero between calls): the 8 claim counters of the in-kernel
-// schedule at a fixed offset, then one arrival counter per unit.  Workspace
+// schedule at a fixed offset, then one arrival counter per unit, then
+// kMergeGroups per unit for the two-level merge of long units.  Workspace
 // (scratch): the stream partition's chunk record (stream partition only),
 // then the split partials.
 constexpr size_t kQueueBytes = 8 * pa::kSchedQueueStride * sizeof(uint32_t);
 size_t counter_region(int units) {
-  return align_up(kQueueBytes) + align_up((size_t)units * sizeof(uint32_t));
+  return align_up(kQueueBytes) + align_up((size_t)units * (1 + pa::kMergeGroups) * sizeof(uint32_t));
 }
 
 struct WsLayout {

@@ -207,13 +207,41 @@ __device__ __forceinline__ void write_out_item(half_t* __restrict__ out, size_t 
   *reinterpret_cast<uint2*>(out + out_base + (size_t)h * D + 4 * c) = pk;
 }
 
+// Where a merge puts its items: the normalised fp16 output rows of the unit.
+template <int D>
+struct OutSink {
+  half_t* out;
+  size_t base;
+  __device__ __forceinline__ void operator()(int h, int c, float, float L, f4_t A) const {
+    write_out_item<D>(out, base, h, c, L, A);
+  }
+};
+
+// ... or one partial (the fold of a group of splits, relative to its max) in
+// the slot behind `racc`.  The (max, sum) pairs wait in LDS (`ml_lds`, two
+// floats per head) until every thread has read the group's own pairs, since
+// the destination slot is one of the group's: store_slot_ml writes them after
+// a barrier.  Each accumulator item is read and rewritten by one thread only.
+template <int D>
+struct SlotSink {
+  __amdgpu_buffer_rsrc_t racc;
+  float* ml_lds;
+  __device__ __forceinline__ void operator()(int h, int c, float M, float L, f4_t A) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, A), racc, (h * D + 4 * c) * 4,
+                                           0, kPolicyDevice);
+    if (c == 0) {
+      ml_lds[2 * h] = M;
+      ml_lds[2 * h + 1] = L;
+    }
+  }
+};
+
 // Items (head, 4-dim chunk) tid * NI .. + NI - 1, + THREADS * NI, ... of a unit:
 // NI consecutive chunks of one head per thread (D / 4 is a multiple of NI).
-template <int D, int THREADS, bool COHERENT, int NI, int SB, typename SlotOf>
+template <int D, int THREADS, bool COHERENT, int NI, int SB, typename SlotOf, typename Sink>
 __device__ __forceinline__ void merge_splits_by(const float* __restrict__ pacc,
-                                                const float* __restrict__ pml,
-                                                half_t* __restrict__ out, SlotOf slot_of, int gt,
-                                                size_t out_base, int ns, int tid) {
+                                                const float* __restrict__ pml, SlotOf slot_of,
+                                                int gt, int ns, int tid, const Sink& sink) {
   constexpr int CH = D / 4;
   static_assert(CH % NI == 0, "a thread's chunks lie in one head");
   const int nitems = gt * CH;
@@ -225,31 +253,30 @@ __device__ __forceinline__ void merge_splits_by(const float* __restrict__ pacc,
     for (int i = 0; i < NI; ++i) A[i] = (f4_t){0.f, 0.f, 0.f, 0.f};
     fold_splits<D, COHERENT, NI, SB>(pacc, pml, slot_of, gt, h, c0, ns, M, L, A);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) write_out_item<D>(out, out_base, h, c0 + i, L, A[i]);
+    for (int i = 0; i < NI; ++i) sink(h, c0 + i, M, L, A[i]);
   }
 }
 
-// Merge the `ns` partials of one unit (gt heads) and write its fp16 output
-// rows, without LDS or barriers.  With more items than threads each thread
-// takes 2 or 4 consecutive chunks of one head: they share the (m, l) loads,
-// and all of a batch's loads are in flight together (up to about 24 per
-// thread), so the round trips a thread waits for are ceil(ns / SB) rather
-// than one per 8 splits and chunk.  The batch follows ns: the re-read
-// padding of a short last batch costs load slots (config 2, 4 splits: 16-split
-// batches measured 3-4% slower than 4-split ones).  Same box, against one
-// chunk per thread in batches of 8: bench config 3 warp_int8 50.4 -> 48.6
-// us, MQA 32/1 INT8 of config 5 44.8 -> 42.6 us.
-template <int D, int THREADS, bool COHERENT, typename SlotOf>
-__device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
-                                             const float* __restrict__ pml,
-                                             half_t* __restrict__ out, SlotOf slot_of, int gt,
-                                             size_t out_base, int ns) {
+// Merge the `ns` partials of one unit (gt heads) into `sink`, without LDS or
+// barriers.  With more items than threads each thread takes 2 or 4
+// consecutive chunks of one head: they share the (m, l) loads, and all of a
+// batch's loads are in flight together (up to about 24 per thread), so the
+// round trips a thread waits for are ceil(ns / SB) rather than one per 8
+// splits and chunk.  The batch follows ns: the re-read padding of a short last
+// batch costs load slots (config 2, 4 splits: 16-split batches measured 3-4%
+// slower than 4-split ones).  Same box, against one chunk per thread in
+// batches of 8: bench config 3 warp_int8 50.4 -> 48.6 us, MQA 32/1 INT8 of
+// config 5 44.8 -> 42.6 us.
+template <int D, int THREADS, bool COHERENT, typename SlotOf, typename Sink>
+__device__ __forceinline__ void merge_splits_into(const float* __restrict__ pacc,
+                                                  const float* __restrict__ pml, SlotOf slot_of,
+                                                  int gt, int ns, const Sink& sink) {
   constexpr int CH = D / 4;
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));   // nothing lane-dependent is hoisted out of a caller's loop
   const int nitems = gt * CH;
 #define PA_MERGE_BY(NI, SB) \
-  merge_splits_by<D, THREADS, COHERENT, NI, SB>(pacc, pml, out, slot_of, gt, out_base, ns, tid)
+  merge_splits_by<D, THREADS, COHERENT, NI, SB>(pacc, pml, slot_of, gt, ns, tid, sink)
   if constexpr (CH % 4 == 0) {
     if (nitems > 2 * THREADS) {
       if (ns <= 4) PA_MERGE_BY(4, 4);
@@ -269,6 +296,15 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
   else if (ns <= 8) PA_MERGE_BY(1, 8);
   else PA_MERGE_BY(1, 16);
 #undef PA_MERGE_BY
+}
+
+// Merge the `ns` partials of one unit and write its fp16 output rows.
+template <int D, int THREADS, bool COHERENT, typename SlotOf>
+__device__ __forceinline__ void merge_splits(const float* __restrict__ pacc,
+                                             const float* __restrict__ pml,
+                                             half_t* __restrict__ out, SlotOf slot_of, int gt,
+                                             size_t out_base, int ns) {
+  merge_splits_into<D, THREADS, COHERENT>(pacc, pml, slot_of, gt, ns, OutSink<D>{out, out_base});
 }
 
 // Block ids of one split: at most max_partition_per_4_waves(D) * NW / 4 tokens,
@@ -961,6 +997,38 @@ __device__ __forceinline__ void merge_wave_states(const Smem& sm, int ct, int nh
   }
 }
 
+// Two-level split merge of the single launches (see decode_split): units of
+// at least kMerge2MinSplits splits whose partials hold at least
+// kMerge2MinFloats accumulator values (256 KB) fold in kMergeGroups groups
+// first.  Smaller merges are faster in one level: the second level adds an
+// acknowledged store and an arrival to the end of the launch (8 sequences of
+// 4096 tokens at 8/1 heads, 32 splits of 8 heads: 12.2 -> 12.5 us in two).
+constexpr int kMerge2MinSplits = 12;
+constexpr int kMerge2MinFloats = 64 * 1024;
+static_assert(kMerge2MinSplits >= 2 * kMergeGroups, "every group holds two splits or more");
+// First split of merge group gi of a unit of ns splits (gi = kMergeGroups: ns);
+// split sp belongs to group sp * kMergeGroups / ns.
+__device__ __forceinline__ int merge_group_first(int gi, int ns) {
+  return (gi * ns + kMergeGroups - 1) / kMergeGroups;
+}
+
+// Waits until this thread's stores are acknowledged, then counts the
+// work-group's arrival at *c (thread 0).  True, in every thread, for the
+// work-group that arrives last of n.
+template <typename Smem>
+__device__ __forceinline__ bool arrive_last(Smem& sm, uint32_t* c, int n) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm.last = prev == (uint32_t)(n - 1);
+  }
+  __syncthreads();
+  return sm.last;
+}
+
 // The decode of one split of one unit by a whole work-group.  FUSED:
 // a unit with one split writes its output here; partials are written
 // device-coherent and the last work-group of the unit merges them (single
@@ -1126,28 +1194,61 @@ __device__ __forceinline__ void decode_split(
   }
   if constexpr (FUSED) {
     if (ns_eff > 1) {
-      // Wait until this thread's partial stores are acknowledged, then count
-      // the arrival; the last work-group of the unit merges every split.
-      // (An arrival counted before the stores, so that the last work-group
-      // could keep its own partial in registers, measured slower: the last
-      // one then waits for the others' stores, by device-scope polling.)
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(0);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        const uint32_t prev =
-            __hip_atomic_fetch_add(cnt + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm.last = prev == (uint32_t)(ns_eff - 1);
+      // Each thread's partial stores are acknowledged before the arrival is
+      // counted; the last work-group to arrive merges.  (An arrival counted
+      // before the stores, so that the last work-group could keep its own
+      // partial in registers, measured slower: the last one then waits for
+      // the others' stores, by device-scope polling.)  A unit of few splits
+      // or small partials has one counter and its last work-group merges
+      // every split.  Larger merges take two levels, so that no
+      // single work-group reads all the partials (one CU's bandwidth bound
+      // that fold: 8 x 32k tokens at 32/1 heads spent 12 of 42 us in it):
+      // the splits form kMergeGroups groups of consecutive splits, each
+      // with its own counter; the last arrival of a group folds the group's
+      // partials into the group's first slot, then counts one arrival at the
+      // unit's counter, whose last arrival folds the groups' slots into the
+      // output.  Every counter is back at zero when the unit is done.
+      const size_t slot0 = wk.slot0, stride = wk.stride;
+      auto slot_of = [=](int sp) { return slot0 + (size_t)sp * stride; };
+      const bool two = ns_eff >= kMerge2MinSplits && ns_eff * gt * D >= kMerge2MinFloats;
+      uint32_t* const cu = cnt + unit;
+      uint32_t* cg = cu;
+      int lo = 0, hi = ns_eff;
+      if (two) {   // (the divisions stay off the one-level path: it ends every launch)
+        const int grp = split * kMergeGroups / ns_eff;
+        lo = merge_group_first(grp, ns_eff);
+        hi = merge_group_first(grp + 1, ns_eff);
+        const size_t n_units = (size_t)sh.num_seqs * sh.num_kv_heads * sh.nchunk;
+        cg = cnt + n_units + (size_t)unit * kMergeGroups + grp;
       }
-      __syncthreads();
-      if (sm.last) {
-        const size_t slot0 = wk.slot0, stride = wk.stride;
-        merge_splits<D, NW * kWave, true>(
-            pacc, pml, out, [=](int sp) { return slot0 + (size_t)sp * stride; }, gt, out_base,
-            ns_eff);
-        if (threadIdx.x == 0)
-          __hip_atomic_store(cnt + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (arrive_last(sm, cg, hi - lo)) {
+        if (!two) {
+          merge_splits<D, NW * kWave, true>(pacc, pml, out, slot_of, gt, out_base, ns_eff);
+        } else {
+          static_assert(NW * 16 >= 2 * 16 * CT, "(max, sum) of every head of the tile fit sm.m");
+          const size_t dst = slot_of(lo);
+          float* const ml_lds = &sm.m[0][0];
+          // (one batch shape for both levels: the code of the whole merge
+          // stays small, and it runs cold at the end of the launch)
+          merge_splits_by<D, NW * kWave, true, 2, 8>(
+              pacc, pml, [=](int i) { return slot_of(lo + i); }, gt, hi - lo, tid,
+              SlotSink<D>{buf_rsrc(pacc + dst * gt * D, (uint32_t)(gt * D * 4)), ml_lds});
+          __syncthreads();   // every thread has read the group's (max, sum) pairs
+          if (tid < gt) {
+            const f2_t ml = {ml_lds[2 * tid], ml_lds[2 * tid + 1]};
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2_t, ml),
+                                                  buf_rsrc(pml + dst * gt * 2, (uint32_t)(gt * 8)),
+                                                  tid * 8, 0, kPolicyDevice);
+          }
+          if (tid == 0) __hip_atomic_store(cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (arrive_last(sm, cu, kMergeGroups))
+            merge_splits_by<D, NW * kWave, true, 2, kMergeGroups>(
+                pacc, pml, [=](int gi) { return slot_of(merge_group_first(gi, ns_eff)); }, gt,
+                kMergeGroups, tid, OutSink<D>{out, out_base});
+          else
+            return;
+        }
+        if (tid == 0) __hip_atomic_store(cu, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }

@@ -29,6 +29,10 @@ constexpr int kMinBlockSize = 8;
 constexpr int kSchedMaxSeqs = 1024;
 constexpr int kSchedItemsPerGroup = 4;
 constexpr int kSchedQueueStride = 32;   // words between the 8 claim counters (128 B)
+// Arrival counters: one per unit, then, for units of many splits (merged in
+// two levels by the single launches), kMergeGroups per unit for the groups
+// of splits.
+constexpr int kMergeGroups = 4;
 
 // Shape of one decode launch, shared by every decode kernel.
 // The decode kernels take (block_table, context_lens, DecodeShape, ...) as

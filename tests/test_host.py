@@ -109,10 +109,11 @@ def test_plan_invariants(lib, s, h, hkv, ctx):
         need = lib.pa_decode_workspace_bytes(kind, s, h, 128, hkv, 16, mb, ctx, 0)
         assert need % 256 == 0 and need > 0
     # counters: the 8 claim counters (1 KB), then one arrival counter per
-    # (sequence, kv head, head chunk of <= 16 query heads)
+    # (sequence, kv head, head chunk of <= 16 query heads) and four per unit
+    # for the groups of a two-level merge
     chunks = -(-(h // hkv) // 16)
     units = s * hkv * chunks
-    assert lib.pa_decode_counter_bytes(s, h, hkv) == 1024 + -(-units * 4 // 256) * 256
+    assert lib.pa_decode_counter_bytes(s, h, hkv) == 1024 + -(-units * 5 * 4 // 256) * 256
     # forced partition sizes are rounded up to 64 tokens
     assert lib.pa_decode_plan(0, s, h, 128, hkv, 16, mb, ctx, 100, ctypes.byref(part),
                               ctypes.byref(ns)) == 0

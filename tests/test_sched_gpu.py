@@ -93,6 +93,26 @@ def test_ragged_fp16_head_dim_256(mode, variant, partition):
 
 
 @pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
+@pytest.mark.parametrize("variant", ["warp", "splitk", "warp_int8", "splitk_int8"])
+def test_two_level_split_merge(mode, variant):
+    """A unit whose split partials hold at least 256 KB of accumulators is
+    merged in two levels: the last split of each of four groups folds its
+    group, the last group folds the four.  32 query heads per kv head
+    (32-head tiles FP16, 16-head INT8) and 64-token splits give units of 70,
+    47 and 33 splits (two levels), 19 (two levels FP16; one INT8, whose
+    partials are half the size), 11 and 1 (one level) in one launch; the
+    second run checks that every counter came back to zero."""
+    _mode(mode)
+    lens = np.array([4480, 2100, 700, 3000, 1, 1200], dtype=np.int32)
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, 32, 1, seed=23)
+    ref = (oracle_int8 if int8 else oracle_fp16)(c)
+    for i in range(2):
+        assert_close(run(c, variant, int8=int8, partition=64), ref,
+                     what=f"mode {mode} {variant} run {i}")
+
+
+@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp_int8", "splitk_int8"])
 @pytest.mark.parametrize("heads", [(16, 8), (32, 1)])
 def test_ragged_int8(mode, variant, heads):
