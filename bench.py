@@ -691,6 +691,13 @@ def run_configs(torch, names, steps, warmup):
                 out[f"cfg4_llama_{ctx // 1024}k_{variant}"] = run_decode_cfg(
                     torch, f"cfg4 {ctx}", lens, 32, 8, 128, variant, steps_for(est, steps),
                     warmup, outliers=True)
+        # Config 4's lengths at MQA 32/1 (an extra line, not a BASELINE config):
+        # 32 splits of 32 heads per sequence, the shape the two-level split
+        # merge is for.
+        for variant in ("splitk", "splitk_int8"):
+            out[f"cfg4_mqa_32k_{variant}"] = run_decode_cfg(
+                torch, "cfg4 MQA 32768", [32768] * 8, 32, 1, 128, variant,
+                steps_for(40, steps), warmup, outliers=True)
     if "cfg5" in names:
         lens = lognormal_lens(256, seed=5)
         for hkv in (8, 1):
