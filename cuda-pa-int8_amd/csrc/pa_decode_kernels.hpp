@@ -220,8 +220,8 @@ struct OutSink {
 // ... or one partial (the fold of a group of splits, relative to its max) in
 // the slot behind `racc`.  The (max, sum) pairs wait in LDS (`ml_lds`, two
 // floats per head) until every thread has read the group's own pairs, since
-// the destination slot is one of the group's: store_slot_ml writes them after
-// a barrier.  Each accumulator item is read and rewritten by one thread only.
+// the destination slot is one of the group's: the caller stores them after a
+// barrier.  Each accumulator item is read and rewritten by one thread only.
 template <int D>
 struct SlotSink {
   __amdgpu_buffer_rsrc_t racc;
