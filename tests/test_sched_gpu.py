@@ -112,6 +112,24 @@ def test_two_level_split_merge(mode, variant):
                      what=f"mode {mode} {variant} run {i}")
 
 
+@pytest.mark.parametrize("mode", [GRID, SCHED])
+@pytest.mark.parametrize("variant,head_dim", [("warp", 128), ("splitk", 128), ("warp", 256),
+                                              ("warp_int8", 128), ("splitk_int8", 128)])
+@pytest.mark.parametrize("scale", [-0.09, 0.0])
+def test_nonpositive_scale(mode, variant, head_dim, scale):
+    """The softmax scale may be zero (equal weights over the valid tokens) or
+    negative (the scores' order reverses); masked tails in the last chunks of
+    ragged lengths must still get zero weight (32 query heads per kv head:
+    32-head tiles FP16 at 128 dims)."""
+    _mode(mode)
+    lens = np.array([1, 37, 300, 1000, 77], dtype=np.int32)
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, 32, 1, head_dim=head_dim, seed=29)
+    c = dict(c, scale=scale)
+    ref = (oracle_int8 if int8 else oracle_fp16)(c)
+    assert_close(run(c, variant, int8=int8), ref, what=f"mode {mode} {variant} D={head_dim}")
+
+
 @pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
 @pytest.mark.parametrize("variant", ["warp_int8", "splitk_int8"])
 @pytest.mark.parametrize("heads", [(16, 8), (32, 1)])
