@@ -1210,7 +1210,8 @@ __device__ __forceinline__ void decode_split(
       // output.  Every counter is back at zero when the unit is done.
       const size_t slot0 = wk.slot0, stride = wk.stride;
       auto slot_of = [=](int sp) { return slot0 + (size_t)sp * stride; };
-      const bool two = ns_eff >= kMerge2MinSplits && ns_eff * gt * D >= kMerge2MinFloats;
+      const bool two =
+          ns_eff >= kMerge2MinSplits && (int64_t)ns_eff * gt * D >= kMerge2MinFloats;
       uint32_t* const cu = cnt + unit;
       uint32_t* cg = cu;
       int lo = 0, hi = ns_eff;
