@@ -5,18 +5,22 @@ A step is one decode call over one batch (all sequences, all heads).  The
 headline workload is BASELINE config 2: Qwen2.5-1.5B-shape GQA 12/2,
 head_dim 128, 32 sequences x 4096 tokens, FP16 KV, single-launch kernel.
 ``value`` is its algorithmic HBM bytes per step / time per step (GB/s).
-The other BASELINE configs are measured the same way and reported under
-``configs`` (INT8 vs FP16, long-context split-K, ragged serving mix,
-quantize + cache-write, the tiny CPU-runnable case), next to a dense
-baseline (SDPA over K/V gathered into contiguous tensors, as the
-reference's bench_paged_decode.py:131-145 does).
+The other BASELINE configs are measured the same way (INT8 vs FP16,
+long-context split-K, ragged serving mix, quantize + cache-write, the tiny
+CPU-runnable case), next to a dense baseline (SDPA over K/V gathered into
+contiguous tensors, as the reference's bench_paged_decode.py:131-145 does).
+The stdout line carries the headline, its roofline, the CPU baseline and a
+[us, fraction of peak] summary per measurement; the full per-config record
+(plans, correctness gates, address-stream probes, read ceilings) goes to
+--detail-out and to the stderr lines.
 
 Timing: W eager warm-up steps, then the K steps are captured in one HIP
 graph (each step reads a different copy of the cache when one copy would
-fit in the 256 MB Infinity Cache) and replayed once untimed; the timed
-region is one replay of exactly K steps, bracketed by synchronize() and
-HIP events on the stream the kernels run on.  The no-sync entry is timed
-(the reference's ``context_lens.min().item()`` host check is skipped).
+fit in the 256 MB Infinity Cache) and replayed once untimed; a timed region
+is one replay of exactly K steps, bracketed by synchronize() and HIP events
+on the stream the kernels run on, and a measurement is the median of three
+such replays (five for the headline).  The no-sync entry is timed (the
+reference's ``context_lens.min().item()`` host check is skipped).
 
     python bench.py [--steps K] [--warmup W] [--configs cfg2,cfg3,...]
 """
@@ -475,6 +479,29 @@ def gather_dense(torch, case, lens, num_heads):
     return k, v
 
 
+def dense_attention_fn(torch, q, k, v, scale):
+    """(fn, impl): fn() computes dense attention of q [S, H, 1, D] over
+    contiguous K/V [S, H, ctx, D] in fp16.  SDPA on its flash or
+    memory-efficient backend; if neither takes the shape, an fp16 matmul form
+    over contiguous operands (softmax in fp32) stands in, and impl names it."""
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        def dense():
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
+        dense()
+        torch.cuda.synchronize()
+        return dense, "sdpa"
+    except RuntimeError:
+        kt = k.transpose(-1, -2).contiguous()
+
+        def dense():
+            p = torch.softmax(torch.matmul(q, kt).float() * scale, dim=-1).to(torch.float16)
+            return torch.matmul(p, v)
+        return dense, "fp16 matmul (q k^T, softmax in fp32, p v), contiguous operands"
+
+
 def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=False):
     """Dense attention over gathered, GQA-repeated K/V (the reference's SDPA
     ceiling, bench_paged_decode.py:131-145), timed with plain launches next to
@@ -488,24 +515,9 @@ def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=Fal
     k, v = gather_dense(torch, case, lens, h)
     q = case["q"].unsqueeze(2)                                   # [S, H, 1, D]
     scale = case["scale"]
-    impl = "sdpa"
-    try:
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-
-        def dense():
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                return torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
-        ref = dense()
-        torch.cuda.synchronize()
-    except RuntimeError:
-        impl = "fp16 matmul (q k^T, softmax in fp32, p v), contiguous operands"
-        kt = k.transpose(-1, -2).contiguous()
-
-        def dense():
-            p = torch.softmax(torch.matmul(q, kt).float() * scale, dim=-1).to(torch.float16)
-            return torch.matmul(p, v)
-        ref = dense()
-        torch.cuda.synchronize()
+    dense, impl = dense_attention_fn(torch, q, k, v, scale)
+    ref = dense()
+    torch.cuda.synchronize()
     for _ in range(warmup):
         dense()
     ms_dense = time_eager(torch, [dense], steps)
@@ -691,6 +703,11 @@ def run_configs(torch, names, steps, warmup):
                 out[f"cfg4_llama_{ctx // 1024}k_{variant}"] = run_decode_cfg(
                     torch, f"cfg4 {ctx}", lens, 32, 8, 128, variant, steps_for(est, steps),
                     warmup, outliers=True)
+                # the reference's partition size as BASELINE states config 4
+                # (kernels/paged_attention_v4_splitk.cu:24), beside the planner's
+                out[f"cfg4_llama_{ctx // 1024}k_{variant}_p512"] = run_decode_cfg(
+                    torch, f"cfg4 {ctx} P=512", lens, 32, 8, 128, variant,
+                    steps_for(est, steps), warmup, outliers=True, partition=512)
         # Config 4's lengths at MQA 32/1 (an extra line, not a BASELINE config):
         # 32 splits of 32 heads per sequence, the shape the two-level split
         # merge is for.
@@ -858,12 +875,10 @@ def _cpu_baseline_timed(seconds, threads, np, ref, metrics):
     seq_ms = med / n_seq * 1e3
     return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=int(threads),
                 kind="port",
-                sample=(f"numpy oracle (oracle/paged_decode_ref.py) on config-2 sequences "
-                        f"(4096 tokens, 12/2 heads, D=128, fp16 cache widened to fp32), "
-                        f"{n_seq} per call, median of {len(calls)} calls after one warm-up "
-                        f"({dt:.1f} s); {seq_ms:.2f} ms per sequence, "
-                        f"{seq_ms * 32:.1f} ms per 32-sequence step; BLAS limited to "
-                        f"{threads} threads, the gather and widening run on one"),
+                sample=(f"numpy oracle on config-2 sequences (4096 tokens, 12/2 heads, D=128, "
+                        f"fp16 widened to fp32), {n_seq} per call, median of {len(calls)} calls "
+                        f"in {dt:.1f} s: {seq_ms:.2f} ms per sequence, {seq_ms * 32:.1f} ms "
+                        f"per 32-sequence step; BLAS on {threads} threads, gather on one"),
                 host_cpus=os.cpu_count(), cpu_model=_cpu_model())
 
 
@@ -888,6 +903,136 @@ def _cpu_model():
     return None
 
 
+# --------------------------------------------------------------------------- the line
+
+LINE_LIMIT = 4096          # bytes of the final stdout line, kept well inside what the driver reads
+HEADLINE_REPLAYS = 5       # the headline is the median of this many K-step graph replays
+
+
+def _finite(x, nd):
+    """x rounded to nd places, or None when it is missing or not finite."""
+    if x is None:
+        return None
+    x = float(x)
+    return round(x, nd) if math.isfinite(x) else None
+
+
+def summarize(configs, peak_gbs=8000.0):
+    """{name: [us, fraction of HBM peak]} for every timed decode or write entry
+    of `configs`, and {name: INT8 us / FP16 us} for each shape timed both ways.
+    Entries without a time (counter launches, length statistics) are left out;
+    the end-to-end bridge is summarized by its time per output token."""
+    out, ratios = {}, {}
+    for name, r in configs.items():
+        if not isinstance(r, dict):
+            continue
+        if "rows" in r:                                       # the reference's A100 shapes
+            for row in r["rows"]:
+                key = "ref_b{}_{}_{}_{}".format(row["seqs"], row["total_tokens"] // row["seqs"],
+                                                row["heads"], row["variant"])
+                out[key] = [_finite(row.get("us"), 2), _finite(row.get("frac_peak"), 4)]
+            continue
+        if "us" in r:
+            frac = r.get("frac_peak")
+            if frac is None and r.get("gbs") is not None:
+                frac = r["gbs"] / peak_gbs
+            out[name] = [_finite(r["us"], 2), _finite(frac, 4)]
+            continue
+        tpots = {k: v["tpot_ms"] for k, v in r.items() if isinstance(v, dict) and "tpot_ms" in v}
+        for k, v in tpots.items():
+            out[f"{name}_{k}_tpot_ms"] = [_finite(v, 3), None]
+    for name, r in out.items():
+        if "_int8" in name:
+            fp_name = name.replace("_int8", "", 1)
+            fp = out.get(fp_name)
+            if fp and fp[0] and r[0]:
+                ratios[fp_name] = round(r[0] / fp[0], 3)
+    if configs.get("cfg3_qwen_int8") and configs.get("cfg3_qwen_fp16_same_shape"):
+        ratios["cfg3_qwen"] = round(configs["cfg3_qwen_int8"]["us"]
+                                    / configs["cfg3_qwen_fp16_same_shape"]["us"], 3)
+    return out, ratios
+
+
+def headline_line(steps, warmup, head, configs, traffic, cpu, peak_gbs=8000.0):
+    """The one JSON object bench.py prints on stdout: the headline (config 2,
+    single launch, FP16), its roofline, the CPU baseline and a [us, frac]
+    summary of every other measurement.  Per-config detail (plans, gates,
+    probes, ceilings) goes to the side file and the stderr lines instead, so
+    the line stays under LINE_LIMIT bytes."""
+    ms = head["us"] / 1e3
+    nbytes = head["algo_bytes"]
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    summary, ratios = summarize(configs, peak_gbs)
+    cpu_short = None
+    if cpu is not None:
+        cpu_short = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample") if k in cpu}
+        if cpu.get("cpu_model"):
+            cpu_short["cpu_model"] = cpu["cpu_model"]
+    probe = head.get("address_stream_probe") or {}
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: fp16 N(0,1) q/K/V, random-permuted block tables; INT8 caches "
+                "written by the quantize kernel",
+        "config": {
+            "workload": "BASELINE config 2: Qwen2.5-1.5B-shape GQA 12/2, head_dim 128, "
+                        "block_size 16, 32 seqs x 4096 ctx, FP16 KV, single launch "
+                        "(paged_decode_attn_warp)",
+            "algo_bytes_per_step": nbytes,
+            "timing": f"median of {HEADLINE_REPLAYS} replays of a {steps}-step HIP graph, "
+                      f"{head.get('cache_copies')} cache copies rotated, no host sync",
+            "gate": {"ok": head.get("ok"),
+                     "headroom": _finite((head.get("gate") or {}).get("headroom"), 4)},
+            "decode_over_probe": _finite(probe.get("decode_over_probe"), 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": peak_gbs,
+            "unit": "GB/s",
+            "frac": round(achieved / peak_gbs, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu_short,
+        "summary_us_frac": summary,
+        "int8_over_fp16": ratios,
+    }
+    # Past the limit, the reference-shape rows go first, then the bridge's times,
+    # then the latest entries (all stay in the side file and on stderr).
+    for prefix in ("ref_", "e2e"):
+        if len(json.dumps(line, allow_nan=False)) <= LINE_LIMIT:
+            break
+        for d in (summary, ratios):
+            for k in [k for k in d if k.startswith(prefix)]:
+                del d[k]
+    while len(json.dumps(line, allow_nan=False)) > LINE_LIMIT and (summary or ratios):
+        (ratios or summary).popitem()
+    return line
+
+
+def write_detail(path, detail):
+    """The full per-config record beside the line (plans, gates, probes,
+    ceilings); a failure to write it is reported and does not end the run."""
+    if not path:
+        return
+    try:
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(detail, f, indent=1, default=str)
+        log(f"[bench] per-config detail written to {path}")
+    except OSError as e:
+        log(f"[bench] could not write {path}: {e}")
+
+
 # --------------------------------------------------------------------------- main
 
 def main():
@@ -905,6 +1050,8 @@ def main():
                          "(used under rocprofv3 counter collection)")
     ap.add_argument("--pmc-copy", action="store_true",
                     help="also run a 256 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--detail-out", default=os.path.join("gpurun_out", "bench_detail.json"),
+                    help="file for the full per-config record ('' to skip)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -930,11 +1077,9 @@ def main():
     # ---- headline: config 2, single-launch FP16
     lens = [4096] * 32
     head = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "warp", args.steps, args.warmup,
-                          replays=1, eager=True, eager_only=args.eager, probe=True)
+                          replays=HEADLINE_REPLAYS, eager=True, eager_only=args.eager,
+                          probe=True)
     head_sk = run_decode_cfg(torch, "cfg2", lens, 12, 2, 128, "splitk", args.steps, args.warmup)
-    ms = head["us"] / 1e3
-    nbytes = head["algo_bytes"]
-    achieved = nbytes / (ms * 1e-3) / 1e9
 
     configs = {"cfg2_qwen_fp16_warp": head, "cfg2_qwen_fp16_splitk": head_sk}
     if args.pmc_copy:
@@ -962,43 +1107,10 @@ def main():
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline(args.cpu_seconds)
 
-    line = {
-        "metric": METRIC,
-        "value": round(achieved, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic: fp16 N(0,1) q/K/V, random-permuted block tables, INT8 caches "
-                "quantized from N(0,1) by the write kernel",
-        "config": {
-            "workload": "BASELINE config 2: Qwen2.5-1.5B-shape GQA decode, 12 q / 2 kv heads, "
-                        "head_dim 128, block_size 16, 32 seqs x 4096 ctx, FP16 KV, "
-                        "single-launch kernel (paged_decode_attn_warp)",
-            "seqs": 32, "context": 4096, "heads": "12/2", "head_dim": 128, "block_size": 16,
-            "algo_bytes_per_step": nbytes,
-            "timed_entry": "no host sync (context-length check skipped), HIP graph of K steps",
-            "cache_copies_rotated": head["cache_copies"],
-            "parallelism": "single GPU",
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": metrics.MI355X_HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / metrics.MI355X_HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-        },
-        "cpu_baseline": cpu,
-        "read_ceiling": ceiling,
-        "configs": configs,
-    }
-    print(json.dumps(line), flush=True)
+    line = headline_line(args.steps, args.warmup, head, configs, traffic, cpu)
+    write_detail(args.detail_out, dict(line=line, configs=configs, read_ceiling=ceiling,
+                                       cpu_baseline_full=cpu))
+    print(json.dumps(line, allow_nan=False), flush=True)
 
 
 if __name__ == "__main__":

@@ -28,11 +28,18 @@
 //
 // INT8 (paged_attention_v5_warp_int8.cu:80-108 semantics): int8 K and V are
 //   converted to fp16 holding 1152 + value (exact, 3 ops per 4 values); the K
-//   bias is removed from the scores with 1152*sum(q) per head and the V bias
-//   with a packed fp16 subtraction.  s_k multiplies each score; s_v is folded
-//   into the fp16 softmax weight, scaled by 2^e with e chosen per iteration
-//   from the largest s_v so the weights stay normal and below fp16's range;
-//   the running sum l accumulates the unscaled weight.
+//   bias is removed from the scores with 1152*sum(q) per head.  V enters the
+//   PV products biased: each chunk's weight sums sum(w) per head come from
+//   one more MFMA against a ones operand, and 1152*sum(w) is subtracted from
+//   the fp32 accumulator after the chunk's products, so no bias carries from
+//   one chunk to the next.  That subtraction cancels in fp32: the chunk's
+//   biased sums are at most 1279*sum(w), so its error stays within a few
+//   roundings of 2^-24 * 1279 * sum(w), below 2.3e-4 times the weight-averaged
+//   s_v in the output (about 2e-6 of a token's largest |v| = 127 s_v).  s_k
+//   multiplies each score; s_v is folded into the fp16 softmax weight, scaled
+//   by 2^e with e chosen per iteration from the largest s_v so the weights
+//   stay normal and below fp16's range; the running sum l accumulates the
+//   unscaled weight.
 //
 // Splits: FUSED (the single-launch warp variant) writes per-split partials
 //   with device-coherent (write-through) stores, waits for them, counts

@@ -39,7 +39,9 @@ struct Counters {
 };
 std::mutex g_counters_mu;
 std::map<std::pair<int, void*>, Counters> g_counters;
-constexpr size_t kMinCounterBytes = 256 << 10;   // 65k units: grows only for huge batches
+// 256 KB: the 1 KB claim-counter block, then 20 bytes per unit (one arrival
+// counter and four merge-group counters), about 13k units; grows only for huge batches.
+constexpr size_t kMinCounterBytes = 256 << 10;
 
 bool stream_capturing(hipStream_t stream) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;

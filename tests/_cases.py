@@ -78,6 +78,31 @@ def oracle_int8(c):
                                       scale=c["scale"], block_size=c["block_size"])
 
 
+def subset_oracle(case, seqs):
+    """The oracle's output for sequences `seqs` of a device case built by
+    bench.make_case: their blocks are gathered on the device, copied to the
+    host and renumbered, so the oracle sees only what it needs."""
+    import torch
+
+    bs, lens = case["bs"], case["lens"]
+    kc, vc, ks, vs = case["caches"][0]
+    nblk = [(lens[s] + bs - 1) // bs for s in seqs]
+    ids = torch.cat([case["bt"][s, :n].long() for s, n in zip(seqs, nblk)])
+    bt = np.zeros((len(seqs), max(nblk)), np.int32)
+    off = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = np.arange(off, off + n)
+        off += n
+    k = kc.index_select(0, ids).cpu().numpy()
+    v = vc.index_select(0, ids).cpu().numpy()
+    if ks is not None:
+        k, v = ref.dequantize_kv(k, v, ks.index_select(0, ids).cpu().numpy(),
+                                 vs.index_select(0, ids).cpu().numpy())
+    q = case["q"].cpu().numpy()[list(seqs)]
+    sub_lens = np.array([lens[s] for s in seqs], np.int32)
+    return ref.paged_decode_attention(q, k, v, bt, sub_lens, scale=case["scale"], block_size=bs)
+
+
 def assert_close(out, expect, atol=ATOL, rtol=RTOL, what=""):
     """Elementwise |out - expect| <= atol + rtol * |expect|.  Returns the
     headroom ratio max(|out - expect| / (atol + rtol * |expect|)): 1.0 is the

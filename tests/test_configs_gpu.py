@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from _cases import assert_close, record_headroom
+from _cases import assert_close, record_headroom, subset_oracle
 from oracle import paged_decode_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -52,28 +52,6 @@ def run(case, variant, check=False):
                    case["bs"], check=check, **kw)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
-
-
-def subset_oracle(case, seqs):
-    """The oracle's output for sequences `seqs` of a device case: their blocks
-    are gathered on the device, copied to the host and renumbered."""
-    bs, lens = case["bs"], case["lens"]
-    kc, vc, ks, vs = case["caches"][0]
-    nblk = [(lens[s] + bs - 1) // bs for s in seqs]
-    ids = torch.cat([case["bt"][s, :n].long() for s, n in zip(seqs, nblk)])
-    bt = np.zeros((len(seqs), max(nblk)), np.int32)
-    off = 0
-    for i, n in enumerate(nblk):
-        bt[i, :n] = np.arange(off, off + n)
-        off += n
-    k = kc.index_select(0, ids).cpu().numpy()
-    v = vc.index_select(0, ids).cpu().numpy()
-    if ks is not None:
-        k, v = ref.dequantize_kv(k, v, ks.index_select(0, ids).cpu().numpy(),
-                                 vs.index_select(0, ids).cpu().numpy())
-    q = case["q"].cpu().numpy()[list(seqs)]
-    sub_lens = np.array([lens[s] for s in seqs], np.int32)
-    return ref.paged_decode_attention(q, k, v, bt, sub_lens, scale=case["scale"], block_size=bs)
 
 
 def check(case, variant, seqs, config, what, **extra):
@@ -154,6 +132,39 @@ def test_config4_long_context(ctx, variant):
     int8 = variant.endswith("int8")
     case = make_case([ctx] * 8, 32, 8, int8=int8, outliers=True, seed=4)
     check(case, variant, [0, 7], "cfg4", f"{variant} 8 x {ctx} 32/8 outliers", ctx=ctx)
+
+
+@pytest.mark.parametrize("variant", ["splitk", "splitk_int8"])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_config4_reference_partition(variant, mode):
+    """Config 4 as BASELINE states it, with the reference's partition size
+    (PARTITION_SIZE 512, kernels/paged_attention_v4_splitk.cu:24): 8 x 32768,
+    32/8 heads, 1% outliers x20, 64 splits per sequence, under the automatic
+    choice (0), the host grid with its reduce launch (1), the in-kernel
+    schedule with the two-level in-launch merge (2) and the stream partition
+    (3); the first and last sequence checked."""
+    import pa_int8
+
+    int8 = variant.endswith("int8")
+    case = make_case([32768] * 8, 32, 8, int8=int8, outliers=True, seed=4)
+    part, ns = pa_int8.decode_plan(variant, 8, 32, 128, 8, 16, case["bt"].shape[1], 0, 512)
+    assert (part, ns) == (512, 64)
+    kc, vc, ks, vs = case["caches"][0]
+    kw = {} if ks is None else dict(k_scales=ks, v_scales=vs)
+    out = torch.empty_like(case["q"])
+    assert pa_int8.capi().pa_decode_set_schedule(mode) == 0
+    try:
+        pa_int8.decode(variant, out, case["q"], kc, vc, case["bt"], case["ctx"], case["scale"],
+                       case["bs"], check=False, partition_tokens=512, **kw)
+        torch.cuda.synchronize()
+    finally:
+        pa_int8.capi().pa_decode_set_schedule(0)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ratio = assert_close(got[[0, 7]], subset_oracle(case, [0, 7]),
+                         what=f"cfg4 {variant} P=512 schedule {mode}")
+    record_headroom("cfg4", f"{variant} 8 x 32768 32/8 outliers P=512 schedule {mode}", ratio,
+                    variant=variant, seqs_checked=2, ctx=32768, partition=512, schedule=mode)
 
 
 @pytest.mark.parametrize("variant", ["warp", "warp_int8"])

@@ -92,24 +92,35 @@ def test_ragged_fp16_head_dim_256(mode, variant, partition):
                  what=f"mode {mode} {variant} partition {partition}")
 
 
-@pytest.mark.parametrize("mode", [GRID, SCHED, STREAM])
+# Two-level merge bound per head_dim: a unit folds in two levels from
+# max(12, 65536 / (heads per tile * head_dim)) splits.  With 32 query heads on
+# one kv head and 64-token splits, the lengths below give units of 70, 47, 33,
+# 19, 11 and 1 splits.  Per tile: FP16 at head_dim <= 128 serves 32 heads
+# (two levels from 32 splits at 64 dims, 26 at 80, 16 at 128); INT8 serves 32
+# in the grid form and 16 under the schedule (64, 52 and 32 splits); head_dim
+# 256 serves 16 (16 splits) and reads its query from LDS.
+TWO_LEVEL_LENS = [4480, 2100, 700, 3000, 1, 1200]
+
+
+@pytest.mark.parametrize("mode,head_dim", [(m, d) for m in (GRID, SCHED)
+                                            for d in (64, 80, 128, 256)] + [(STREAM, 128)])
 @pytest.mark.parametrize("variant", ["warp", "splitk", "warp_int8", "splitk_int8"])
-def test_two_level_split_merge(mode, variant):
+def test_two_level_split_merge(mode, head_dim, variant):
     """A unit whose split partials hold at least 256 KB of accumulators is
     merged in two levels: the last split of each of four groups folds its
-    group, the last group folds the four.  32 query heads per kv head
-    (32-head tiles FP16, 16-head INT8) and 64-token splits give units of 70,
-    47 and 33 splits (two levels), 19 (two levels FP16; one INT8, whose
-    partials are half the size), 11 and 1 (one level) in one launch; the
-    second run checks that every counter came back to zero."""
+    group, the last group folds the four.  Units of one and two levels meet
+    in one launch (TWO_LEVEL_LENS); the second run checks that every counter
+    came back to zero.  The stream partition merges the split-K kinds in its
+    reduce launch (and runs the single-launch kinds on the grid), so it is
+    run at head_dim 128 only."""
     _mode(mode)
-    lens = np.array([4480, 2100, 700, 3000, 1, 1200], dtype=np.int32)
+    lens = np.array(TWO_LEVEL_LENS, dtype=np.int32)
     int8 = variant.endswith("int8")
-    c = (int8_case if int8 else fp16_case)(len(lens), lens, 32, 1, seed=23)
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, 32, 1, head_dim=head_dim, seed=23)
     ref = (oracle_int8 if int8 else oracle_fp16)(c)
     for i in range(2):
         assert_close(run(c, variant, int8=int8, partition=64), ref,
-                     what=f"mode {mode} {variant} run {i}")
+                     what=f"mode {mode} {variant} D={head_dim} run {i}")
 
 
 @pytest.mark.parametrize("mode", [GRID, SCHED])
