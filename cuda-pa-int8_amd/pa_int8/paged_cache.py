@@ -2,9 +2,10 @@
 
 Mirrors ``PagedKVCache`` of benchmarks/int8_bridge/paged_cache.py:41-182: the
 same constructor, attributes (``k_cache``, ``v_cache``, ``k_scales``,
-``v_scales``, ``block_table``, ``lengths``), methods and byte accounting, for
-batch 1 with an identity block table.  The three variants are the
-reference's:
+``v_scales``, ``block_table``, ``lengths``), methods and byte figures, for
+batch 1 with an identity block table.  The tensors, their sizes and the tail
+clearing all follow one ``PagedLayout`` (per-block shapes of the kernels'
+layouts).  The three variants are the reference's:
 
 * ``"fp16"``            -- fp16 cache (write: ``reshape_and_cache``);
 * ``"int8_per_token"``  -- int8 cache, one fp32 scale per (token, kv head)
@@ -26,6 +27,8 @@ as the reference does (:111).
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import registry
@@ -33,11 +36,55 @@ from . import registry
 VARIANTS = ("fp16", "int8_per_token", "int8_per_tensor")
 
 
+@dataclass(frozen=True)
+class PagedLayout:
+    """Geometry of one layer's paged tensors, as the write and decode kernels
+    address them: per tensor, the shape of one physical block, its dtype and
+    the axis (within the block) that runs over the block's token slots.
+
+    K ``[Hkv, D/x, bs, x]`` and V ``[Hkv, D, bs]`` in fp16 or int8; with INT8,
+    one fp32 scale per (kv head, slot) for K and for V ``[Hkv, bs]``.  Every
+    size the cache reports is read off these per-block shapes."""
+
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    x: int
+    int8: bool
+
+    def blocks_for(self, tokens):
+        return -(-int(tokens) // self.block_size)
+
+    def tensors(self):
+        """{name: (per-block shape, dtype, token axis)} in allocation order."""
+        h, d, bs, x = self.num_kv_heads, self.head_dim, self.block_size, self.x
+        store = torch.int8 if self.int8 else torch.float16
+        spec = {"k_cache": ((h, d // x, bs, x), store, 2),
+                "v_cache": ((h, d, bs), store, 2)}
+        if self.int8:
+            spec["k_scales"] = ((h, bs), torch.float32, 1)
+            spec["v_scales"] = ((h, bs), torch.float32, 1)
+        return spec
+
+    def block_bytes(self):
+        """Bytes of one physical block over every tensor of one layer."""
+        total = 0
+        for shape, dtype, _ in self.tensors().values():
+            n = 1
+            for e in shape:
+                n *= e
+            total += n * torch.empty((), dtype=dtype).element_size()
+        return total
+
+
 class PagedKVCache:
     def __init__(self, num_layers, num_kv_heads, head_dim, max_len, block_size=16, x=8,
                  variant="fp16", device="cuda"):
-        assert variant in VARIANTS
-        assert head_dim % x == 0
+        # (AssertionError, as the reference's constructor raises for these)
+        if variant not in VARIANTS:
+            raise AssertionError(f"variant must be one of {VARIANTS}, got {variant!r}")
+        if head_dim % x:
+            raise AssertionError(f"head_dim {head_dim} is not a multiple of x = {x}")
         self.num_layers = num_layers
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
@@ -46,32 +93,27 @@ class PagedKVCache:
         self.variant = variant
         self.is_int8 = variant != "fp16"
         self.device = device
-
-        self.num_blocks = (max_len + block_size - 1) // block_size
-        store = torch.int8 if self.is_int8 else torch.float16
-        self.k_cache = torch.zeros(num_layers, self.num_blocks, num_kv_heads, head_dim // x,
-                                   block_size, x, dtype=store, device=device)
-        self.v_cache = torch.zeros(num_layers, self.num_blocks, num_kv_heads, head_dim,
-                                   block_size, dtype=store, device=device)
-        if self.is_int8:
-            self.k_scales = torch.zeros(num_layers, self.num_blocks, num_kv_heads, block_size,
-                                        dtype=torch.float32, device=device)
-            self.v_scales = torch.zeros(num_layers, self.num_blocks, num_kv_heads, block_size,
-                                        dtype=torch.float32, device=device)
-            self._k_tensor_scale = [None] * num_layers
-            self._v_tensor_scale = [None] * num_layers
-        # identity block table (batch 1), shared by every layer
+        self.layout = PagedLayout(num_kv_heads, head_dim, block_size, x, self.is_int8)
+        self.num_blocks = self.layout.blocks_for(max_len)
+        # k_cache, v_cache (and k_scales, v_scales): [num_layers, num_blocks, *block shape]
+        for name, (shape, dtype, _) in self.layout.tensors().items():
+            setattr(self, name, torch.zeros((num_layers, self.num_blocks) + shape, dtype=dtype,
+                                            device=device))
+        # batch 1: sequence block j is physical block j in every layer, so slot t is token t
         self.block_table = torch.arange(self.num_blocks, dtype=torch.int32,
                                         device=device).view(1, -1)
-        # slot ids 0 .. num_blocks * block_size - 1: slot t is token t
         self._slots = torch.arange(self.num_blocks * block_size, dtype=torch.int64, device=device)
-        self.lengths = [0] * num_layers
+        self.reset()
 
     def reset(self):
+        """Every layer empty again; per-tensor scales are taken anew at the next prefill."""
         self.lengths = [0] * self.num_layers
         if self.is_int8:
             self._k_tensor_scale = [None] * self.num_layers
             self._v_tensor_scale = [None] * self.num_layers
+
+    def _tensors(self):
+        return [getattr(self, name) for name in self.layout.tensors()]
 
     # --- write path ---------------------------------------------------------
 
@@ -115,11 +157,9 @@ class PagedKVCache:
         off = L % self.block_size
         if off:
             blk = L // self.block_size
-            self.k_cache[layer_idx, blk, :, :, off:, :].zero_()
-            self.v_cache[layer_idx, blk, :, :, off:].zero_()
-            if self.is_int8:
-                self.k_scales[layer_idx, blk, :, off:].zero_()
-                self.v_scales[layer_idx, blk, :, off:].zero_()
+            for name, (_, _, tok_axis) in self.layout.tensors().items():
+                getattr(self, name)[layer_idx, blk].narrow(tok_axis, off,
+                                                           self.block_size - off).zero_()
         self.lengths[layer_idx] = L
 
     def decode_append(self, layer_idx, k, v):
@@ -141,21 +181,11 @@ class PagedKVCache:
         return torch.tensor([self.lengths[layer_idx]], dtype=torch.int32, device=self.device)
 
     def kv_bytes(self):
-        """Bytes of the whole K/V allocation (and scales) (paged_cache.py:161-170)."""
-        b = self.k_cache.element_size() * self.k_cache.nelement()
-        b += self.v_cache.element_size() * self.v_cache.nelement()
-        if self.is_int8:
-            b += self.k_scales.element_size() * self.k_scales.nelement()
-            b += self.v_scales.element_size() * self.v_scales.nelement()
-        return b
+        """Bytes of the whole allocation: K, V and (INT8) their scales, every
+        layer and block (paged_cache.py:161-170)."""
+        return sum(t.numel() * t.element_size() for t in self._tensors())
 
     def kv_bytes_for_len(self, n):
-        """Bytes K+V (and int8 scales) need for `n` tokens over all layers
-        (paged_cache.py:172-182)."""
-        blocks = (n + self.block_size - 1) // self.block_size
-        elem = 1 if self.is_int8 else 2
-        per_blk = 2 * self.num_kv_heads * self.head_dim * self.block_size
-        b = blocks * per_blk * elem * self.num_layers
-        if self.is_int8:
-            b += blocks * 2 * self.num_kv_heads * self.block_size * 4 * self.num_layers
-        return b
+        """Bytes that `n` tokens occupy over all layers: whole blocks, each
+        with its K, V and scale slots (paged_cache.py:172-182)."""
+        return self.layout.blocks_for(n) * self.layout.block_bytes() * self.num_layers

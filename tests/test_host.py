@@ -344,6 +344,19 @@ def test_paged_cache_class_host_logic():
     assert fp16.kv_bytes_for_len(2048) == fp16.kv_bytes()
     assert i8.kv_bytes_for_len(2048) == i8.kv_bytes()
     assert i8.kv_bytes_for_len(17) == 2 * 28 * (2 * 2 * 128 * 16 + 2 * 2 * 16 * 4)
+    # every figure follows the allocated tensors' per-block sizes
+    for cache in (fp16, i8):
+        per_block = sum(t[0, 0].numel() * t.element_size()
+                        for t in (cache.k_cache, cache.v_cache) +
+                        ((cache.k_scales, cache.v_scales) if cache.is_int8 else ()))
+        assert cache.layout.block_bytes() == per_block
+        assert cache.kv_bytes_for_len(1) == per_block * 28
+        assert cache.kv_bytes_for_len(0) == 0
+        assert cache.kv_bytes_for_len(33) == 3 * per_block * 28
+    with pytest.raises(AssertionError):
+        pa_int8.PagedKVCache(variant="int4", **kw)
+    with pytest.raises(AssertionError):
+        pa_int8.PagedKVCache(variant="fp16", **dict(kw, head_dim=100))
     c = pa_int8.PagedKVCache(variant="int8_per_tensor", **kw)
     assert c.context_lens(3).tolist() == [0] and c.lengths == [0] * 28
     with pytest.raises(RuntimeError, match="CUDA"):
