@@ -675,6 +675,32 @@ def run_cfg5_counter_launches(torch, launches=8):
     return dict(launches=done, note="plain launches for rocprofv3 counters; not timed")
 
 
+def run_counter_launches(torch, launches=8):
+    """Plain launches (no timing, no gate) of the decode kernels whose stalls
+    the counter summaries break down: config 2 `warp`, config 3 `warp_int8`,
+    config 4 32k `splitk_int8`, config 4's lengths at MQA 32/1 (both kinds),
+    then config 5's four launches (run_cfg5_counter_launches)."""
+    done = []
+    for name, lens, h, hkv, variant, outliers in (
+            ("cfg2", [4096] * 32, 12, 2, "warp", False),
+            ("cfg3", [8192] * 64, 12, 2, "warp_int8", False),
+            ("cfg4 32k", [32768] * 8, 32, 8, "splitk_int8", True),
+            ("mqa 8x32k", [32768] * 8, 32, 1, "splitk", True),
+            ("mqa 8x32k", [32768] * 8, 32, 1, "splitk_int8", True)):
+        case = make_case(torch, lens, h, hkv, 128, 16, "cuda", 0, variant.endswith("int8"),
+                         outliers, 1)
+        fns, _ = decode_steps(torch, case, variant)
+        for _ in range(launches):
+            fns[0]()
+        torch.cuda.synchronize()
+        done.append(f"{name} {variant} x{launches}")
+        log(f"[bench] counter launches: {done[-1]}")
+        del case, fns
+        torch.cuda.empty_cache()
+    done += run_cfg5_counter_launches(torch, launches)["launches"]
+    return dict(launches=done, note="plain launches for rocprofv3 counters; not timed")
+
+
 def run_configs(torch, names, steps, warmup):
     import numpy as np
 
@@ -726,6 +752,8 @@ def run_configs(torch, names, steps, warmup):
                                 distribution="lognormal(ln 1024, 1.0) clipped [16, 32768], seed 5")
     if "cfg5counters" in names:
         out["cfg5_counter_launches"] = run_cfg5_counter_launches(torch)
+    if "counters" in names:
+        out["counter_launches"] = run_counter_launches(torch)
     if "refshapes" in names:
         rows = []
         for b, ctx, h, hkv, variant, a100_us, src in REF_SHAPES:
@@ -1042,7 +1070,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="all",
                     help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'; also "
-                    "cfg5counters (config 5's decode launches for rocprofv3 counters, untimed)")
+                    "cfg5counters (config 5's decode launches for rocprofv3 counters, untimed), "
+                    "counters (those and the other kernels the counter summaries cover)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",

@@ -33,7 +33,7 @@ probe_decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, De
                     const uint8_t* __restrict__ vc, const float* __restrict__ ksc,
                     const float* __restrict__ vsc, uint32_t* __restrict__ sink) {
   constexpr int D = kProbeD;
-  using Wave = DecodeWave<D, 1, I8>;
+  using Wave = DecodeWave<D, 1, I8, !I8 && NTL>;   // the grid decode's lane mapping
   using Blocks = typename Wave::Blocks;
   constexpr int PAIRS = Wave::PAIRS;
   constexpr int IT = Wave::IT;
@@ -90,6 +90,18 @@ probe_decode_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl, De
   __builtin_amdgcn_s_barrier();
 
   auto load_blocks = [&](int it_, Blocks& b) {
+    if constexpr (!I8 && NTL) {   // as decode_split's group mapping
+      const int tok0 = t_begin + it_ * IT;
+#pragma unroll
+      for (int m = 0; m < Wave::NG; ++m) {
+        const int g0 = tok0 + 16 * m;
+        const int gs = g0 < t_end ? g0 : t_begin;
+        const int lo = (gs >> bsl) - b_first, hi = ((gs + 8) >> bsl) - b_first;
+        b.gb[2 * m] = __builtin_amdgcn_readfirstlane(blk[lo < nblk ? lo : 0]);
+        b.gb[2 * m + 1] = __builtin_amdgcn_readfirstlane(blk[hi < nblk ? hi : 0]);
+      }
+      return;
+    }
     int kt[PAIRS], vt[PAIRS];
     dw.block_tokens(t_begin + it_ * IT, t_end, t_begin, kt, vt);
 #pragma unroll
