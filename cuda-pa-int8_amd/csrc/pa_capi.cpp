@@ -50,8 +50,10 @@ constexpr int kTargetWaves = 2048;   // waves one decode launch aims for (256 CU
 constexpr int kMinPartition = 256;   // per 4 waves: one 64-token iteration each
 // Shortest item of the in-kernel schedule on ragged lengths, in tokens at
 // head_dim <= 128 (half that above, where a token holds twice the bytes),
-// whatever the group size.
+// whatever the group size; FP16 in 8-wave groups (one per CU) goes down to
+// kSchedMinItemTokensF16.
 constexpr int kSchedMinItemTokens = 2048;
+constexpr int kSchedMinItemTokensF16 = 1536;
 // Test and tuning overrides (pa_mi355x_tuning.h), per calling thread.
 thread_local int g_waves_override = 0;
 thread_local int g_schedule_mode = 0;   // 0 auto, 1 grid, 2 in-kernel schedule
@@ -229,8 +231,14 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
       // Shorter items pay their fixed start-up and merge costs too often
       // (forced-partition sweeps of bench config 5 on MI355X, same box: 2048
       // against 1024 tokens, INT8 in 4-wave groups, 32/8 161.9 -> 156.2 us,
-      // MQA 32/1 41.2 -> 39.7 us; FP16 in 8-wave groups was already at 2048).
-      p.pmin = head_dim <= 128 ? kSchedMinItemTokens : kSchedMinItemTokens / 2;
+      // MQA 32/1 41.2 -> 39.7 us).  FP16 in 8-wave groups, one per CU, has
+      // half the work-groups and gains from 1536 where the floor binds (MQA
+      // 32/1, same box: config 5 56.2 -> 54.2 us; lognormal mixes of 512 x
+      // median 512 60.1 -> 56.1 and 64 x median 2048 36.2 -> 33.0; 128 x
+      // median 4096 108.9 -> 111.1); with 8 kv heads the floor does not bind.
+      const int floor_tokens =
+          (is_f16(kind) && p.waves == 8) ? kSchedMinItemTokensF16 : kSchedMinItemTokens;
+      p.pmin = head_dim <= 128 ? floor_tokens : floor_tokens / 2;
       // Equal lengths: one item per resident work-group, down to the grid
       // plan's bound (config 2 would otherwise run on half the work-groups).
       p.pmin_uniform = kMinPartition * p.waves / 4;
@@ -433,7 +441,7 @@ const char* pa_status_string(pa_status_t s) {
     case PA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case PA_ERR_BAD_SHAPE: return "tensor sizes are inconsistent or out of range";
     case PA_ERR_BAD_BLOCK_SIZE: return "block_size must divide TILE and be a multiple of 8 (16 for int8)";
-    case PA_ERR_UNSUPPORTED: return "head_dim must be 64, 80, 96, 112, 128 or 256 and x must be 8";
+    case PA_ERR_UNSUPPORTED: return "head_dim must be a multiple of 16 in [32, 256] and x must be 8";
     case PA_ERR_WORKSPACE: return "counters or workspace NULL, misaligned or smaller than required";
     case PA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
     case PA_ERR_EMPTY_CONTEXT: return "context_lens must be >= 1 (empty sequences unsupported)";

@@ -382,7 +382,7 @@ struct CacheView {
 // same stream: its block id is looked up the same way) and masked.
 template <int D, int CT, bool I8, bool GM = false>
 struct DecodeWave {
-  static_assert(D % 16 == 0 && D >= 64 && D <= 256, "head_dim: a multiple of 16 in [64, 256]");
+  static_assert(D % 16 == 0 && D >= 32 && D <= 256, "head_dim: a multiple of 16 in [32, 256]");
   static_assert(CT == 1 || (CT == 2 && D <= 128), "two column tiles only for head_dim <= 128");
   static constexpr int KC = (D + 31) / 32;   // 32-dim k-chunks of one QK product
   static constexpr int NT = D / 16;          // 16-dim output tiles of PV

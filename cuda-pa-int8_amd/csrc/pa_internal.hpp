@@ -129,10 +129,12 @@ pa_status_t decode_sizes_capped(const DecodeCall& c, size_t ws_cap, size_t* coun
 pa_status_t decode_launch_capped(const DecodeCall& c, void* counters, size_t counter_bytes,
                                  void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-// Head dims the library is built for.  The decode kernels are instantiated
+// Head dims the library is built for: every multiple of 16 in [32, 256].  The decode kernels are instantiated
 // once per head_dim from pa_decode_inst.hip (compiled with -DPA_HEAD_DIM=D);
 // the write kernels take the same set.
-#define PA_FOR_EACH_HEAD_DIM(X) X(64) X(80) X(96) X(112) X(128) X(256)
+#define PA_FOR_EACH_HEAD_DIM(X)                                                          \
+  X(32) X(48) X(64) X(80) X(96) X(112) X(128) X(144) X(160) X(176) X(192) X(208) X(224) X(240) \
+  X(256)
 
 // Per head_dim D: the launcher of every decode kind, and the resident
 // work-groups of a persistent decode kernel (the in-kernel schedule, or the

@@ -16,8 +16,8 @@
  *   block_table   [num_seqs, max_blocks_per_seq]                       int32
  *   context_lens  [num_seqs]                                           int32
  * All arrays are dense and row-major.  kv_head of query head h is
- * h / (num_heads / num_kv_heads).  head_dim is one of 64, 80, 96, 112, 128
- * and 256.
+ * h / (num_heads / num_kv_heads).  head_dim is a multiple of 16 in [32, 256]
+ * (the reference takes any multiple of 8, kernels/paged_attention_v3_warp.cu:48-58).
  *
  * Behaviour on data the host cannot see (the caller owns these guarantees;
  * the kernels stay memory-safe when they are broken):
