@@ -677,14 +677,17 @@ def run_cfg5_counter_launches(torch, launches=8):
 
 def run_counter_launches(torch, launches=8):
     """Plain launches (no timing, no gate) of the decode kernels whose stalls
-    the counter summaries break down: config 2 `warp`, config 3 `warp_int8`,
-    config 4 32k `splitk_int8`, config 4's lengths at MQA 32/1 (both kinds),
-    then config 5's four launches (run_cfg5_counter_launches)."""
+    the counter summaries break down: config 2 `warp`, config 3 `warp_int8`
+    and `warp`, config 4 32k `splitk_int8` and `splitk`, config 4's lengths at
+    MQA 32/1 (both kinds), then config 5's four launches
+    (run_cfg5_counter_launches)."""
     done = []
     for name, lens, h, hkv, variant, outliers in (
             ("cfg2", [4096] * 32, 12, 2, "warp", False),
             ("cfg3", [8192] * 64, 12, 2, "warp_int8", False),
+            ("cfg3", [8192] * 64, 12, 2, "warp", False),
             ("cfg4 32k", [32768] * 8, 32, 8, "splitk_int8", True),
+            ("cfg4 32k", [32768] * 8, 32, 8, "splitk", True),
             ("mqa 8x32k", [32768] * 8, 32, 1, "splitk", True),
             ("mqa 8x32k", [32768] * 8, 32, 1, "splitk_int8", True)):
         case = make_case(torch, lens, h, hkv, 128, 16, "cuda", 0, variant.endswith("int8"),
