@@ -31,11 +31,12 @@ cache_write_f16_kernel(const half_t* __restrict__ key, const half_t* __restrict_
                        const int64_t* __restrict__ slots, int num_tokens, int num_kv_heads,
                        half_t* __restrict__ kc, half_t* __restrict__ vc, int num_blocks, int bs,
                        int bs_log2, int njobs) {
-  static_assert(D % 16 == 0, "head_dim must be a multiple of 16");
+  static_assert(D % 8 == 0, "head_dim must be a multiple of 8");
   constexpr int DG = D / 8;            // 8-dim groups of a row
   constexpr int JQ = (DG + 3) / 4;     // 16-B groups per lane: dim groups (l >> 4) + 4j
-  // (with head_dim % 32 == 16 the last j is a group only for lanes l >> 4 < 2;
-  // the others load the row's last group, in bounds, and store nothing)
+  // (with head_dim % 32 != 0 the last j is a group only for lanes with
+  // (l >> 4) + 4j < DG; the others load the row's last group, in bounds, and
+  // store nothing)
   __shared__ __attribute__((aligned(16))) half_t tile[kWriteWaves][D * 16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -441,7 +441,7 @@ const char* pa_status_string(pa_status_t s) {
     case PA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case PA_ERR_BAD_SHAPE: return "tensor sizes are inconsistent or out of range";
     case PA_ERR_BAD_BLOCK_SIZE: return "block_size must divide TILE and be a multiple of 8 (16 for int8)";
-    case PA_ERR_UNSUPPORTED: return "head_dim must be a multiple of 16 in [32, 256] and x must be 8";
+    case PA_ERR_UNSUPPORTED: return "head_dim must be a multiple of 8 in [8, 256] and x must be 8";
     case PA_ERR_WORKSPACE: return "counters or workspace NULL, misaligned or smaller than required";
     case PA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
     case PA_ERR_EMPTY_CONTEXT: return "context_lens must be >= 1 (empty sequences unsupported)";

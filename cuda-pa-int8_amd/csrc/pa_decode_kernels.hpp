@@ -382,16 +382,21 @@ struct CacheView {
 // same stream: its block id is looked up the same way) and masked.
 template <int D, int CT, bool I8, bool GM = false>
 struct DecodeWave {
-  static_assert(D % 16 == 0 && D >= 32 && D <= 256, "head_dim: a multiple of 16 in [32, 256]");
+  static_assert(D % 8 == 0 && D >= 8 && D <= 256, "head_dim: a multiple of 8 in [8, 256]");
   static_assert(CT == 1 || (CT == 2 && D <= 128), "two column tiles only for head_dim <= 128");
   static constexpr int KC = (D + 31) / 32;   // 32-dim k-chunks of one QK product
-  static constexpr int NT = D / 16;          // 16-dim output tiles of PV
+  static constexpr int NT = (D + 15) / 16;   // 16-dim output tiles of PV
   static constexpr int DG = D / 8;           // 8-dim groups of a K row
-  // With head_dim % 32 == 16 the last k-chunk holds 16 dims: its dim groups
-  // 4(KC-1) + g for g >= 2 lie past the row.  Those lanes load the row's last
-  // group instead (in bounds) and feed zeros to the MFMA; their query
-  // operand is zero as well.
+  // With head_dim % 32 != 0 the last k-chunk holds 8, 16 or 24 dims: its dim
+  // groups 4(KC-1) + g with 4(KC-1) + g >= DG lie past the row.  Those lanes
+  // load the row's last group instead (in bounds) and feed zeros to the MFMA;
+  // their query operand is zero as well.
   static constexpr bool KPAD = (D % 32) != 0;
+  // With head_dim % 16 == 8 the last output tile holds 8 dims: its V rows r
+  // >= 8 lie past the row.  Those lanes load row r - 8 instead (in bounds);
+  // the products land in accumulator rows 8..15 of the tile (lanes g >= 2),
+  // which are never stored.
+  static constexpr bool VPAD = (D % 16) != 0;
   // 32-token pairs per chunk: two, except with head_dim 256 (whose
   // accumulators are twice as large) and with two column tiles (whose query
   // operands, scores and accumulators are twice as many); either way the
@@ -504,10 +509,23 @@ struct DecodeWave {
     }
   }
 
-  // QLDS: the query operand of k-chunk kk from the staged tile.
+  // QLDS: the query operand of k-chunk kk from the staged tile.  The padding
+  // lanes of a short last chunk would read past the row's D halves (the row's
+  // unwritten pad, or the next row); they take zeros, since whatever bits lie
+  // there could be an fp16 NaN or infinity, and 0 * NaN poisons the MFMA sum.
   __device__ __forceinline__ h8_t q_operand(int ct, int kk) const {
-    if constexpr (QLDS) return *reinterpret_cast<const h8_t*>(qs + r * QROW + 32 * kk + 8 * g);
-    else return qreg[ct][kk];
+    if constexpr (QLDS) {
+      if (KPAD && kk == KC - 1 && 4 * kk + g >= DG) return (h8_t){};
+      return *reinterpret_cast<const h8_t*>(qs + r * QROW + 32 * kk + 8 * g);
+    } else {
+      return qreg[ct][kk];
+    }
+  }
+
+  // V row of output tile t that lane (r, g) loads, relative to dim r: 16t,
+  // or for the padding rows of a half last tile 16t - 8 (see VPAD).
+  __device__ __forceinline__ int vdim(int t) const {
+    return (VPAD && t == NT - 1 && r >= 8) ? 16 * t - 8 : 16 * t;
   }
 
   // INT8: the K bias of each head, once the query operand has arrived.
@@ -695,7 +713,7 @@ struct DecodeWave {
   __device__ __forceinline__ void issue_v(const CacheView& cv, const VPlan& v) {
     if constexpr (W8) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) vw[t] = load_tile<uint4, NTL>(v.vp[0] + (size_t)(16 * t) * cv.bs);
+      for (int t = 0; t < NT; ++t) vw[t] = load_tile<uint4, NTL>(v.vp[0] + (size_t)vdim(t) * cv.bs);
       return;
     }
     if constexpr (GM) {
@@ -705,8 +723,8 @@ struct DecodeWave {
         nv2[p][1] = v.nv2[p][1];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const uint2 lo = load_tile<uint2, NTL>(v.vp2[p][0] + (size_t)(16 * t) * cv.bs * 2);
-          const uint2 hi = load_tile<uint2, NTL>(v.vp2[p][1] + (size_t)(16 * t) * cv.bs * 2);
+          const uint2 lo = load_tile<uint2, NTL>(v.vp2[p][0] + (size_t)vdim(t) * cv.bs * 2);
+          const uint2 hi = load_tile<uint2, NTL>(v.vp2[p][1] + (size_t)vdim(t) * cv.bs * 2);
           vr[p][t] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
       }
@@ -717,7 +735,7 @@ struct DecodeWave {
       nvalid[p] = v.nvalid[p];
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        vr[p][t] = load_tile<LVec, NTL>(v.vp[p] + (size_t)(16 * t) * cv.bs * ESZ);
+        vr[p][t] = load_tile<LVec, NTL>(v.vp[p] + (size_t)vdim(t) * cv.bs * ESZ);
       if constexpr (I8) {
         const float4 a0 = *reinterpret_cast<const float4*>(cv.ksc + v.slot[p]);
         const float4 a1 = *reinterpret_cast<const float4*>(cv.ksc + v.slot[p] + 4);
@@ -997,8 +1015,10 @@ struct DecodeWave {
       sm.l[w][r] = l_run;
     }
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t) {
+      if (VPAD && t == NT - 1 && g >= 2) continue;   // dims past the row (see VPAD)
       *reinterpret_cast<f4_t*>(&sm.a[w][r][16 * t + 4 * g]) = acc[ct][t] * unscale;
+    }
   }
 };
 

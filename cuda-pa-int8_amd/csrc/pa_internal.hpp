@@ -129,12 +129,13 @@ pa_status_t decode_sizes_capped(const DecodeCall& c, size_t ws_cap, size_t* coun
 pa_status_t decode_launch_capped(const DecodeCall& c, void* counters, size_t counter_bytes,
                                  void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-// Head dims the library is built for: every multiple of 16 in [32, 256].  The decode kernels are instantiated
-// once per head_dim from pa_decode_inst.hip (compiled with -DPA_HEAD_DIM=D);
-// the write kernels take the same set.
+// Head dims the library is built for: every multiple of 8 in [8, 256].  The
+// decode kernels are instantiated once per head_dim from pa_decode_inst.hip
+// (compiled with -DPA_HEAD_DIM=D); the write kernels take the same set.
 #define PA_FOR_EACH_HEAD_DIM(X)                                                          \
-  X(32) X(48) X(64) X(80) X(96) X(112) X(128) X(144) X(160) X(176) X(192) X(208) X(224) X(240) \
-  X(256)
+  X(8) X(16) X(24) X(32) X(40) X(48) X(56) X(64) X(72) X(80) X(88) X(96) X(104) X(112)  \
+  X(120) X(128) X(136) X(144) X(152) X(160) X(168) X(176) X(184) X(192) X(200) X(208)   \
+  X(216) X(224) X(232) X(240) X(248) X(256)
 
 // Per head_dim D: the launcher of every decode kind, and the resident
 // work-groups of a persistent decode kernel (the in-kernel schedule, or the

@@ -180,9 +180,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(void* base, uint32_t
 }
 
 // The 16-B input groups of one job for one lane, and the lane's token slot.
-// Lane quarter qq owns the dim groups qq + 4j; with head_dim % 32 == 16 the
-// last j holds a group only for qq < 2 (the others load the row's last group,
-// in bounds, and ignore it).
+// Lane quarter qq owns the dim groups qq + 4j; with head_dim % 32 != 0 the
+// last j holds a group only for qq + 4j < D / 8 (the others load the row's
+// last group, in bounds, and ignore it).
 template <int D>
 struct QuantJob {
   static constexpr int DG = D / 8;          // 8-dim groups of a row
@@ -206,7 +206,7 @@ quant_write_kernel(const uint16_t* __restrict__ key, const uint16_t* __restrict_
                    int8_t* __restrict__ vc, float* __restrict__ ksc, float* __restrict__ vsc,
                    int num_blocks, int bs, int bs_log2, int njobs, const float* __restrict__ k_scale_in,
                    const float* __restrict__ v_scale_in) {
-  static_assert(D % 16 == 0, "head_dim must be a multiple of 16");
+  static_assert(D % 8 == 0, "head_dim must be a multiple of 8");
   constexpr int JQ = QuantJob<D>::JQ;
   constexpr int DG = QuantJob<D>::DG;
   __shared__ __attribute__((aligned(16))) uint8_t tile[kQuantWaves][D * 16];

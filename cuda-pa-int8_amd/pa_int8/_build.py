@@ -36,7 +36,7 @@ PROBE_LIB_NAME = "libpa_bench_probe.so"
 
 # head_dims of the decode kernels: pa_decode_inst.hip is compiled once per
 # entry (keep in step with PA_FOR_EACH_HEAD_DIM in csrc/pa_internal.hpp).
-HEAD_DIMS = tuple(range(32, 257, 16))
+HEAD_DIMS = tuple(range(8, 257, 8))
 HIP_SOURCES = [
     "pa_quant.hip",
     "pa_cache_write.hip",

@@ -16,7 +16,7 @@
  *   block_table   [num_seqs, max_blocks_per_seq]                       int32
  *   context_lens  [num_seqs]                                           int32
  * All arrays are dense and row-major.  kv_head of query head h is
- * h / (num_heads / num_kv_heads).  head_dim is a multiple of 16 in [32, 256]
+ * h / (num_heads / num_kv_heads).  head_dim is a multiple of 8 in [8, 256]
  * (the reference takes any multiple of 8, kernels/paged_attention_v3_warp.cu:48-58).
  *
  * Behaviour on data the host cannot see (the caller owns these guarantees;

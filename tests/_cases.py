@@ -19,8 +19,8 @@ BLOCK_SIZE = 16
 X = 8
 # every head_dim the library is built for (the reference takes any multiple
 # of 8: kernels/paged_attention_v3_warp.cu:48-58; this build takes every
-# multiple of 16 in [32, 256])
-HEAD_DIMS = list(range(32, 257, 16))
+# multiple of 8 in [8, 256])
+HEAD_DIMS = list(range(8, 257, 8))
 
 # tests/test_paged_decode_attn.py:19-22
 CONTEXT_LENS = [1, 15, 16, 17, 31, 128, 500]

@@ -167,18 +167,20 @@ def test_config4_reference_partition(variant, mode):
                     variant=variant, seqs_checked=2, ctx=32768, partition=512, schedule=mode)
 
 
+@pytest.mark.parametrize("head_dim", [128, 72, 200])
 @pytest.mark.parametrize("bs", [8, 16, 32])
 @pytest.mark.parametrize("variant,mode", [("warp", 0), ("splitk", 1)])
-def test_group_mapping_large_fp16(bs, variant, mode):
+def test_group_mapping_large_fp16(bs, variant, mode, head_dim):
     """FP16 grid launches that read more than 32 MB take the group mapping
     (16-token groups per MFMA row tile, each group half at its own block):
     block sizes 8 (a group spans two blocks), 16 and 32, lengths that end
     inside a group and inside a block, on the single launch and the grid
-    form of split-K (its reduce launch); every sequence checked."""
+    form of split-K (its reduce launch); head_dim 72 and 200 add a short
+    last QK chunk and a half last output tile; every sequence checked."""
     import pa_int8
 
     lens = [8192 - 37 * i for i in range(8)]
-    case = _bench().make_case(torch, lens, 12, 2, 128, bs, DEV, 7, False, False, 1)
+    case = _bench().make_case(torch, lens, 12, 2, head_dim, bs, DEV, 7, False, False, 1)
     kc, vc = case["caches"][0][0], case["caches"][0][1]
     assert kc.numel() * 2 * 2 > 32 << 20          # a non-temporal (group-mapped) launch
     out = torch.empty_like(case["q"])
@@ -191,8 +193,9 @@ def test_group_mapping_large_fp16(bs, variant, mode):
         pa_int8.capi().pa_decode_set_schedule(0)
     seqs = list(range(8))
     ratio = assert_close(out.float().cpu().numpy(), subset_oracle(case, seqs),
-                         what=f"{variant} block_size {bs}")
-    record_headroom("group-mapping", f"{variant} 8 ragged x ~8192 12/2 block_size {bs}", ratio)
+                         what=f"{variant} block_size {bs} D={head_dim}")
+    record_headroom("group-mapping", f"{variant} 8 ragged x ~8192 12/2 D={head_dim} block_size {bs}",
+                    ratio)
 
 
 @pytest.mark.parametrize("variant", ["warp", "warp_int8"])

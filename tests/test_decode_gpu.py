@@ -143,10 +143,11 @@ def test_fp16_head_dims(variant, head_dim, clen, num_heads, num_kv_heads):
 
 
 @pytest.mark.parametrize("variant", F16_VARIANTS)
-@pytest.mark.parametrize("head_dim", [80, 96, 112])
+@pytest.mark.parametrize("head_dim", [24, 40, 72, 80, 96, 112, 136, 200])
 def test_fp16_head_dims_forced_splits(variant, head_dim):
-    """Head dims that are not a multiple of 32 (masked last QK chunk) across
-    many splits, both work distributions."""
+    """Head dims that are not a multiple of 32 (masked last QK chunk of 8,
+    16 or 24 dims; with head_dim % 16 == 8 also a half last output tile)
+    across many splits, both work distributions."""
     import pa_int8
 
     lib = pa_int8.capi()

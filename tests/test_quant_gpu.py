@@ -35,7 +35,8 @@ def special_rows(d, rng):
     r = np.zeros(d, np.float32); r[:4] = [1e-7, -3e-7, 6e-8, 0]; rows.append(r)  # scale -> 0
     r = rng.standard_normal(d).astype(np.float32) * 2e-3; rows.append(r)  # subnormal fp16 scale
     r = np.zeros(d, np.float32)
-    r[:12] = [127, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -126.5, 63.5, -0.49]
+    ties = [127, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -126.5, 63.5, -0.49]
+    r[:min(12, d)] = ties[:min(12, d)]
     rows.append(r)                                                          # exact ties, scale 1
     r = rng.standard_normal(d).astype(np.float32); r[0] = 1000.0; rows.append(r)  # outlier
     r = np.full(d, -65504.0, np.float32); r[1::2] = 65504.0; rows.append(r)     # fp16 max

@@ -103,7 +103,8 @@ TWO_LEVEL_LENS = [4480, 2100, 700, 3000, 1, 1200]
 
 
 @pytest.mark.parametrize("mode,head_dim", [(m, d) for m in (GRID, SCHED)
-                                            for d in (64, 80, 128, 256)] + [(STREAM, 128)])
+                                            for d in (64, 72, 80, 128, 200, 256)] +
+                         [(STREAM, 128), (STREAM, 72)])
 @pytest.mark.parametrize("variant", ["warp", "splitk", "warp_int8", "splitk_int8"])
 def test_two_level_split_merge(mode, head_dim, variant):
     """A unit whose split partials hold at least 256 KB of accumulators is
