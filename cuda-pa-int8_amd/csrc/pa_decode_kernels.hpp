@@ -1619,6 +1619,117 @@ __device__ __forceinline__ uint32_t div_q(const DivU32& v, uint32_t n) {
   return (t + ((n - t) >> v.s1)) >> v.s2;
 }
 
+// Inclusive prefix sum over the wave: Hillis-Steele steps inside each
+// 16-lane row by DPP row shifts (a lane shifted in from outside its row reads
+// 0), then the totals of the rows below it, read from lanes 15, 31 and 47.
+// Every lane must be active.
+__device__ __forceinline__ uint32_t wave_scan_dpp(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int row = (threadIdx.x & (kWave - 1)) >> 4;
+  return v + (row > 0 ? r0 : 0u) + (row > 1 ? r1 : 0u) + (row > 2 ? r2 : 0u);
+}
+
+// The schedule of at most 64 sequences, one per lane: every wave derives it
+// on its own with wave-wide reductions and DPP scans, wave 0 writes the
+// tables, and one barrier publishes them; the same schedule, table for table,
+// as build_schedule, whose cross-wave reductions and scans (LDS round trips
+// and barriers) it skips.  Measured on MI355X against build_schedule at the
+// bench's shapes (same box, alternating): config 2 split-K 28.73 -> 27.55 us,
+// config 4 32k INT8 90.43 -> 89.15 (FP16 166.61 -> 165.45), 8 x 32k MQA 35.08
+// -> 34.05 (INT8 28.49 -> 27.15); 128k even.
+template <int NTH>
+__device__ __forceinline__ Schedule build_schedule_small(const int* __restrict__ ctxl,
+                                                         const DecodeShape& sh,
+                                                         const SchedArgs& sa, SchedSmem& ss) {
+  constexpr int NWV = NTH / kWave;
+  const int S = sh.num_seqs;
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool writer = threadIdx.x < kWave;
+  const bool in = lane < S;
+  const int cap = sh.max_blocks * sh.block_size;
+  int c = in ? ctxl[lane] : 0;
+  c = c < 0 ? 0 : (c > cap ? cap : c);
+  // Wave-uniform, read into scalar registers: otherwise the compiler takes
+  // every value derived from them (the partition, the claim classes, the
+  // item fields) as divergent, and the whole item loop grows (214 instead of
+  // 191 VGPRs for the INT8 kernel, 8% slower at config 5's MQA).
+  const uint32_t t = __builtin_amdgcn_readfirstlane(wave_reduce_u(in ? (uint32_t)c >> 10 : 0u, OpAddU()));
+  const uint32_t a = __builtin_amdgcn_readfirstlane(wave_reduce_u(in ? (uint32_t)c : 0xFFFFFFFFu, OpMinU()));
+  const uint32_t b = __builtin_amdgcn_readfirstlane(wave_reduce_u(in ? (uint32_t)c : 0u, OpMaxU()));
+  Schedule sc;
+  sc.uniform = a == b;
+  {
+    constexpr uint64_t kGroupsPerCU = kWavesPerCU / NWV;
+    const uint64_t groups = sc.uniform ? (gridDim.x + kGroupsPerCU - 1) / kGroupsPerCU : gridDim.x;
+    const uint64_t k = sc.uniform ? 1 : kSchedItemsPerGroup;
+    const float want = __builtin_ceilf((float)t * (1024.f * (float)sh.num_kv_heads) /
+                                       (float)(groups * k));
+    uint64_t part = (uint64_t)fminf(want, (float)sa.pmax);
+    part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
+    const uint64_t lo = sc.uniform ? (uint64_t)sa.pmin_uniform : (uint64_t)sa.pmin;
+    part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
+    const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
+    sc.partition = (int)(part < top ? part : top);
+  }
+  while (true) {
+    const int P = sc.partition;
+    const int qv = (int)((uint32_t)c / (uint32_t)P);
+    const int rv = c - qv * P;
+    const bool shortrow = in && (rv != 0 || c == 0);
+    const uint32_t fs = in ? (uint32_t)qv : 0u, ps = shortrow ? 1u : 0u;
+    const uint32_t fi = wave_scan_dpp(fs), pi = wave_scan_dpp(ps);
+    const int tf = __builtin_amdgcn_readlane((int)fi, kWave - 1);
+    const int tp = __builtin_amdgcn_readlane((int)pi, kWave - 1);
+    if (tf + tp > sa.rows_max && P < sa.pmax) {
+      sc.partition = P * 2 < sa.pmax ? P * 2 : sa.pmax;
+      continue;
+    }
+    int bb = -1;
+    if (shortrow) {
+      bb = kShortBuckets - 1;
+#pragma unroll
+      for (int k = 1; k < kShortBuckets; ++k) bb -= (rv * kShortBuckets >= k * P) ? 1 : 0;
+    }
+    // a band's earlier members (in sequence order) and the bands' sizes, two
+    // bands per 32-bit scan (16 bits each)
+    const uint32_t c01 = bb == 0 ? 1u : (bb == 1 ? 0x10000u : 0u);
+    const uint32_t c23 = bb == 2 ? 1u : (bb == 3 ? 0x10000u : 0u);
+    const uint32_t s01 = wave_scan_dpp(c01), s23 = wave_scan_dpp(c23);
+    const uint32_t t01 = (uint32_t)__builtin_amdgcn_readlane((int)s01, kWave - 1);
+    const uint32_t t23 = (uint32_t)__builtin_amdgcn_readlane((int)s23, kWave - 1);
+    if (writer && in) {
+      ss.full_pre[lane] = (int)(fi - fs);
+      ss.part_pre[lane] = (uint16_t)(pi - ps);
+      ss.rem[lane] = (uint16_t)rv;
+      if (bb >= 0) {
+        const int n0 = (int)(t01 & 0xFFFFu), n1 = (int)(t01 >> 16), n2 = (int)(t23 & 0xFFFFu);
+        const uint32_t e01 = s01 - c01, e23 = s23 - c23;   // exclusive
+        int pos;
+        if (bb == 0) pos = (int)(e01 & 0xFFFFu);
+        else if (bb == 1) pos = n0 + (int)(e01 >> 16);
+        else if (bb == 2) pos = n0 + n1 + (int)(e23 & 0xFFFFu);
+        else pos = n0 + n1 + n2 + (int)(e23 >> 16);
+        ss.short_seq[pos] = (uint16_t)lane;
+      }
+    }
+    if (writer && lane == 0) {
+      ss.full_pre[S] = tf;
+      ss.part_pre[S] = (uint16_t)tp;
+    }
+    sc.n_full = tf;
+    sc.n_rows = tf + tp;
+    break;
+  }
+  __syncthreads();
+  return sc;
+}
+
 // Builds the schedule in LDS; every thread of the work-group takes part and
 // returns the same values.  Thread t owns sequences [t*E, t*E + E).
 template <int NTH>
@@ -1808,7 +1919,11 @@ decode_sched_kernel(const int* __restrict__ bt, const int* __restrict__ ctxl,
                 "LDS budget");
   __shared__ DecodeSmem<D, NW> sm;
   __shared__ SchedSmem ss;
-  const Schedule sc = build_schedule<NW * kWave>(ctxl, sh, sa, ss);
+  // (the hint keeps the larger batches' path laid out as the hot one: without
+  // it config 5's INT8 MQA ran 2.5-3.7% slower, with the same registers)
+  Schedule sc;
+  if (__builtin_expect(sh.num_seqs > kWave, 1)) sc = build_schedule<NW * kWave>(ctxl, sh, sa, ss);
+  else sc = build_schedule_small<NW * kWave>(ctxl, sh, sa, ss);
 
   const int S = sh.num_seqs, hkv = sh.num_kv_heads, nchunk = sh.nchunk;
   const int P = __builtin_amdgcn_readfirstlane(sc.partition);

@@ -230,6 +230,31 @@ def test_schedule_zero_and_clamped_context(variant, mode):
     assert_close(got[1:3], oracle_fp16(c2)[1:3], what="clamped")
 
 
+@pytest.mark.parametrize("num_seqs", [1, 63, 64, 65, 130])
+@pytest.mark.parametrize("variant", ["splitk", "splitk_int8"])
+def test_schedule_small_batch_boundary(num_seqs, variant):
+    """Batches of at most 64 sequences take the one-wave schedule build, larger
+    ones the work-group build: both sides of the boundary with ragged lengths,
+    zero lengths, lengths at whole partitions (no short row) and a forced
+    partition that puts short rows in every band."""
+    _mode(SCHED)
+    lens = ragged_lens(num_seqs, seed=num_seqs + 50, hi=4000)
+    if num_seqs > 3:
+        lens[1] = 0
+        lens[2] = 1024
+        lens[3] = 2048
+    int8 = variant.endswith("int8")
+    c = (int8_case if int8 else fp16_case)(num_seqs, np.maximum(lens, 1), 8, 2, seed=19)
+    want = (oracle_int8 if int8 else oracle_fp16)(c)
+    got = run(c, variant, lens=lens, check=False, int8=int8)
+    nz = lens > 0
+    assert np.all(got[~nz] == 0)
+    assert_close(got[nz], want[nz], what=f"{num_seqs} seqs")
+    for p in (256, 1024):
+        got = run(c, variant, lens=lens, check=False, int8=int8, partition=p)
+        assert_close(got[nz], want[nz], what=f"{num_seqs} seqs P={p}")
+
+
 @pytest.mark.parametrize("partition", [64, 320, 2048])
 def test_schedule_forced_partition(partition):
     _mode(SCHED)
