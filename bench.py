@@ -554,16 +554,19 @@ def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=Fal
     return res
 
 
-def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0):
+def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0, long_len=16384):
     """End-to-end greedy decode of a random-init Qwen2.5-1.5B-shape model (fp16,
     28 layers, 12 q / 2 kv heads, head_dim 128, vocab 151936) through the
     transformers bridge: prompt attention by SDPA, every decode step's
     attention by the split-K kernel over the paged cache (reference:
     benchmarks/int8_bridge/run_bridge.py).  Per cache variant: time to first
-    token, time per output token, KV-cache bytes, and agreement with the FP16
-    variant (greedy match; mean |log p| difference on the FP16 continuation,
-    teacher-forced).  No checkpoint is available offline, so perplexity itself
-    is not meaningful here and is not reported."""
+    token, time per output token with eager launches (the reference's way) and
+    with the decode step replayed from a captured HIP graph, KV-cache bytes,
+    and agreement with the FP16 variant (greedy match; mean |log p| difference
+    on the FP16 continuation, teacher-forced).  A second setup decodes after a
+    `long_len`-token prompt, graph replays only, where the cache's bytes are a
+    visible share of each token's reads.  No checkpoint is available offline,
+    so perplexity itself is not meaningful here and is not reported."""
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
     from pa_int8 import PagedKVCache
@@ -579,15 +582,21 @@ def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0):
     model.set_attn_implementation(br.ATTN_NAME)
     g = torch.Generator().manual_seed(seed)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g).cuda()
+    variants = ("fp16", "int8_per_token", "int8_per_tensor")
+
+    def new_cache(variant, n):
+        return PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128, max_len=n,
+                            variant=variant)
+
     res = {}
     ref_tokens = ref_lp = None
     # two passes over the variants; the first pays one-time costs (kernel loads, clock
     # ramp: a first FP16 pass measured 18.8 ms per token, later passes 13.3 ms)
     for rep in range(2):
-        for variant in ("fp16", "int8_per_token", "int8_per_tensor"):
-            cache = PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128,
-                                 max_len=prompt_len + max_new, variant=variant)
+        for variant in variants:
+            cache = new_cache(variant, prompt_len + max_new)
             gen, ttft, tpot, _ = br.generate_greedy(model, prompt, max_new, cache)
+            gen_g, _, tpot_g, _ = br.generate_greedy_graph(model, prompt, max_new, cache)
             if rep == 0:
                 continue
             if ref_tokens is None:
@@ -597,22 +606,42 @@ def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0):
                 ref_lp = lp
             res[variant] = dict(
                 ttft_ms=round(ttft * 1e3, 2), tpot_ms=round(tpot * 1e3, 3),
+                graph_tpot_ms=round(tpot_g * 1e3, 3),
+                graph_tokens_match_eager=round(float((gen_g == gen).float().mean()), 4),
                 kv_bytes=int(cache.kv_bytes_for_len(prompt_len + max_new)),
                 greedy_match_vs_fp16=round(float((gen == ref_tokens).float().mean()), 4),
                 mean_abs_dlogp_vs_fp16=round(float((lp - ref_lp).abs().mean()), 5))
             log(f"[bench] e2e bridge {variant}: TTFT {res[variant]['ttft_ms']} ms, "
-                f"TPOT {res[variant]['tpot_ms']} ms, mean |dlogp| vs fp16 "
-                f"{res[variant]['mean_abs_dlogp_vs_fp16']}")
+                f"TPOT {res[variant]['tpot_ms']} ms eager, {res[variant]['graph_tpot_ms']} ms "
+                f"graph, mean |dlogp| vs fp16 {res[variant]['mean_abs_dlogp_vs_fp16']}")
             del cache
+    g = torch.Generator().manual_seed(seed + 1)
+    prompt = torch.randint(0, cfg.vocab_size, (1, long_len), generator=g).cuda()
+    long = {}
+    for variant in ("fp16",) + variants:   # the first FP16 pass warms the long shapes
+        cache = new_cache(variant, long_len + max_new)
+        _, ttft, tpot_g, _ = br.generate_greedy_graph(model, prompt, max_new, cache)
+        long[variant] = dict(ttft_ms=round(ttft * 1e3, 2), graph_tpot_ms=round(tpot_g * 1e3, 3),
+                             kv_bytes=int(cache.kv_bytes_for_len(long_len + max_new)))
+        del cache
+    for variant in variants:
+        log(f"[bench] e2e bridge, {long_len}-token prompt, {variant}: TTFT "
+            f"{long[variant]['ttft_ms']} ms, TPOT {long[variant]['graph_tpot_ms']} ms graph")
+    res[f"prompt_{long_len}"] = long
     res["setup"] = dict(model="random-init Qwen2.5-1.5B shape (no checkpoint offline), fp16",
-                        prompt_len=prompt_len, max_new=max_new, batch=1,
+                        prompt_len=prompt_len, long_prompt_len=long_len, max_new=max_new,
+                        batch=1,
                         decode_attention="split-K kernel via transformers AttentionInterface",
-                        timing="wall clock per model call, synchronized, eager launches "
-                               "(the 28 layers' host-side launch overhead dominates TPOT)",
+                        timing="wall clock, synchronized: TTFT one prompt call; tpot_ms the "
+                               "mean eager one-token model call (host launches of 28 layers "
+                               "dominate it); graph_tpot_ms the mean per token over replays of "
+                               "the captured decode step, each with one argmax and one id copy",
                         agreement="random weights give nearly flat logits, so one early argmax "
                                   "flip changes every later greedy token: greedy_match is "
                                   "informational; mean_abs_dlogp (teacher-forced on the FP16 "
-                                  "continuation) measures the quantization error")
+                                  "continuation) measures the quantization error; "
+                                  "graph_tokens_match_eager compares the graph replays' greedy "
+                                  "tokens with the eager loop's on the same cache variant")
     del model
     torch.cuda.empty_cache()
     return res
@@ -982,9 +1011,16 @@ def summarize(configs, peak_gbs=8000.0):
                 frac = r["gbs"] / peak_gbs
             out[name] = [_finite(r["us"], 2), _finite(frac, 4)]
             continue
-        tpots = {k: v["tpot_ms"] for k, v in r.items() if isinstance(v, dict) and "tpot_ms" in v}
-        for k, v in tpots.items():
-            out[f"{name}_{k}_tpot_ms"] = [_finite(v, 3), None]
+        # the bridge: per variant, and per variant of a nested setup (a longer prompt)
+        entries = []
+        for k, v in r.items():
+            if isinstance(v, dict):
+                entries.append((f"{name}_{k}", v))
+                entries += [(f"{name}_{k}_{k2}", v2) for k2, v2 in v.items() if isinstance(v2, dict)]
+        for key, v in entries:
+            for field in ("tpot_ms", "graph_tpot_ms"):
+                if field in v:
+                    out[f"{key}_{field}"] = [_finite(v[field], 3), None]
     for name, r in out.items():
         if "_int8" in name:
             fp_name = name.replace("_int8", "", 1)

@@ -175,6 +175,30 @@ class PagedKVCache:
         self.lengths[layer_idx] = t + 1
         return t + 1
 
+    @property
+    def capacity(self):
+        """Token slots per layer."""
+        return self.num_blocks * self.block_size
+
+    def append_at(self, layer_idx, k, v, slot):
+        """Write one token's K/V ``[num_kv_heads, head_dim]`` at the slot that
+        the device tensor `slot` (int64, one element) holds.  This is the
+        append of a captured decode step, whose position lives on the device;
+        the host lengths move with ``advance`` once the step has run."""
+        if self.variant == "int8_per_tensor" and self._k_tensor_scale[layer_idx] is None:
+            raise RuntimeError("int8_per_tensor: prefill sets the layer's scales before appends")
+        if slot.dtype != torch.int64 or slot.numel() != 1 or slot.device != self.k_cache.device:
+            raise TypeError("slot must be a one-element int64 tensor on the cache's device")
+        k = self._kernel_input(k.reshape(1, self.num_kv_heads, self.head_dim))
+        v = self._kernel_input(v.reshape(1, self.num_kv_heads, self.head_dim))
+        self._write(layer_idx, k, v, slot.reshape(1))
+
+    def advance(self, n=1):
+        """Count `n` tokens appended to every layer by ``append_at``."""
+        if any(t + n > self.capacity for t in self.lengths):
+            raise AssertionError("cache is full")
+        self.lengths = [t + n for t in self.lengths]
+
     # --- read path ----------------------------------------------------------
 
     def context_lens(self, layer_idx):

@@ -22,6 +22,13 @@ step appended to the cache and answered by the split-K decode kernel over it
 * A decode step calls the kernel through the no-sync entry: the cache knows
   its length on the host, so no ``context_lens.min()`` device-to-host copy is
   made per layer (the reference's op makes one).
+* ``DecodeGraph`` captures the one-token step (all layers: projections, the
+  cache write and the decode kernel) as one HIP graph whose position and
+  length live on the device; ``generate_greedy_graph`` replays it per token.
+  The eager loop's time per token is the host launching 28 layers' kernels;
+  the replay's is the device's.
+* Every model call computes the logits of its last position only
+  (``logits_to_keep=1``): a 1024-token prompt's full logits would be 0.3 GB.
 """
 
 from __future__ import annotations
@@ -91,6 +98,7 @@ class DecodeSession:
         self.cache = cache
         self.position = 0
         self._token = None
+        self._graph = None         # the DecodeGraph being warmed up or captured
         if getattr(cache, "is_int8", False):
             self._kernel = "splitk_int8"
         else:
@@ -113,7 +121,8 @@ class DecodeSession:
         the last one ([1, vocab])."""
         n = ids.shape[1]
         pos = torch.arange(self.position, self.position + n, device=ids.device).unsqueeze(0)
-        logits = self.model(input_ids=ids, position_ids=pos, use_cache=False).logits[:, -1, :]
+        logits = self.model(input_ids=ids, position_ids=pos, use_cache=False,
+                            logits_to_keep=1).logits[:, -1, :]
         self.position += n
         return logits
 
@@ -127,17 +136,92 @@ class DecodeSession:
             scaling = d ** -0.5
         k_tok = key[0].permute(1, 0, 2)                  # [n, Hkv, D], one row per position
         v_tok = value[0].permute(1, 0, 2)
-        if n > 1:
-            self.cache.prefill(layer, k_tok.contiguous(), v_tok.contiguous())
-            return _prefill_attention(query, key, value, scaling).transpose(1, 2).contiguous()
-        self.cache.decode_append(layer, k_tok[0], v_tok[0])
         c = self.cache
+        if n > 1:
+            if self._graph is not None:
+                raise RuntimeError("a captured decode step feeds one token")
+            c.prefill(layer, k_tok.contiguous(), v_tok.contiguous())
+            return _prefill_attention(query, key, value, scaling).transpose(1, 2).contiguous()
+        if self._graph is None:
+            c.decode_append(layer, k_tok[0], v_tok[0])
+            ctx = c.context_lens(layer)
+        else:   # the position and the length are device buffers the graph advances
+            c.append_at(layer, k_tok[0], v_tok[0], self._graph.slot)
+            ctx = self._graph.ctx
         q = query.reshape(1, h, d).to(torch.float16)
         out = torch.empty_like(q)
         scales = dict(k_scales=c.k_scales[layer], v_scales=c.v_scales[layer]) if c.is_int8 else {}
         registry.decode(self._kernel, out, q, c.k_cache[layer], c.v_cache[layer], c.block_table,
-                        c.context_lens(layer), scaling, c.block_size, check=False, **scales)
+                        ctx, scaling, c.block_size, check=False, **scales)
         return out.view(1, 1, h, d).to(query.dtype)
+
+
+class DecodeGraph:
+    """A session's one-token decode step, captured once as a HIP graph and
+    replayed for every later token.
+
+    The step reads its inputs from device buffers: the token id, its position
+    (also the cache slot it is written to: batch 1, identity block table) and
+    the context length the decode kernel reads.  The graph advances the
+    position and the length itself, so a step is one copy of the id and one
+    replay: no per-layer host work, and no host-to-device copy of a length
+    (the eager step makes one per layer).  Allocations during capture come
+    from torch's graph-private pool; the library's split counters are cleared
+    by a fill kernel, which a graph replays correctly.
+
+    Build it inside the session (``with DecodeSession(...) as s``), after the
+    prompt step.  It stays valid for that pass only: its buffers hold this
+    pass's position, and its kernels this cache's tensors."""
+
+    @torch.no_grad()
+    def __init__(self, session):
+        s = session
+        if s.model is None or s.position == 0:
+            raise RuntimeError("capture a decode step after the prompt step of a session "
+                               "with a model")
+        dev = s.cache.k_cache.device
+        self.session = s
+        self.ids = torch.zeros((1, 1), dtype=torch.long, device=dev)
+        self.pos = torch.full((1, 1), s.position, dtype=torch.long, device=dev)
+        self.slot = self.pos.view(1)
+        self.ctx = torch.full((1,), s.position + 1, dtype=torch.int32, device=dev)
+        self.graph = torch.cuda.CUDAGraph()
+        pos0, ctx0 = self.pos.clone(), self.ctx.clone()
+        s._graph = self
+        try:
+            # One eager pass on a side stream first (lazy library set-up stays out
+            # of the capture).  It writes token 0's K/V at the next slot; the first
+            # replay writes the real token there.
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._body()
+            torch.cuda.current_stream().wait_stream(side)
+            self.pos.copy_(pos0)
+            self.ctx.copy_(ctx0)
+            with torch.cuda.graph(self.graph):
+                self.logits = self._body()
+        finally:
+            s._graph = None
+
+    def _body(self):
+        logits = self.session.model(input_ids=self.ids, position_ids=self.pos, use_cache=False,
+                                    logits_to_keep=1).logits[:, -1, :]
+        self.pos.add_(1)
+        self.ctx.add_(1)
+        return logits
+
+    def step(self, ids):
+        """Feeds ``ids`` ([1, 1] on the device) at the next position; returns the
+        logits of that position ([1, vocab], overwritten by the next step)."""
+        s = self.session
+        if s.position >= s.cache.capacity:
+            raise AssertionError("cache is full")
+        self.ids.copy_(ids)
+        self.graph.replay()
+        s.position += 1
+        s.cache.advance(1)
+        return self.logits
 
 
 def set_active_cache(cache):
@@ -225,6 +309,40 @@ def generate_greedy(model, input_ids, max_new_tokens, cache):
     decode = times[1:]
     tpot = sum(decode) / len(decode) if decode else float("nan")
     return torch.cat(chosen, dim=1), times[0], tpot, seen
+
+
+def generate_greedy_graph(model, input_ids, max_new_tokens, cache, keep_logits=False):
+    """generate_greedy with every one-token step replayed from a captured
+    ``DecodeGraph``.  Returns ``(ids [1, n], ttft_s, tpot_s, step_logits)``:
+    the prompt call's wall time, the mean wall time per token over the
+    replays (the capture excluded; each token costs one replay, one argmax and
+    one id copy, as in the eager loop), and, with `keep_logits`, the logits
+    before every generated token (CPU fp32; reading them back synchronizes)."""
+    chosen, seen = [], []
+    with DecodeSession(model, cache) as s:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits = s.step(input_ids)
+        torch.cuda.synchronize()
+        ttft = time.perf_counter() - t0
+        tpot = float("nan")
+        if keep_logits:
+            seen.append(logits[0].float().cpu())
+        tok = logits.argmax(-1, keepdim=True)
+        chosen.append(tok)
+        if max_new_tokens > 1:
+            g = DecodeGraph(s)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(max_new_tokens - 1):
+                logits = g.step(tok)
+                if keep_logits:
+                    seen.append(logits[0].float().cpu())
+                tok = logits.argmax(-1, keepdim=True)
+                chosen.append(tok)
+            torch.cuda.synchronize()
+            tpot = (time.perf_counter() - t0) / (max_new_tokens - 1)
+    return torch.cat(chosen, dim=1), ttft, tpot, seen
 
 
 def teacher_force_logprobs(model, prompt_ids, cont_ids, cache):

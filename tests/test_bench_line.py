@@ -60,9 +60,13 @@ def _full_configs():
         r.update(a100_us=a100, a100_source=src, a100_over_mi355x_latency=round(a100 / 50.0, 2))
         rows.append(r)
     c["reference_shapes"] = dict(rows=rows, note="z" * 200)
-    c["e2e_qwen_bridge"] = {v: dict(ttft_ms=80.0, tpot_ms=12.1, kv_bytes=1 << 24,
+    c["e2e_qwen_bridge"] = {v: dict(ttft_ms=80.0, tpot_ms=12.1, graph_tpot_ms=0.912,
+                                    graph_tokens_match_eager=1.0, kv_bytes=1 << 24,
                                     greedy_match_vs_fp16=1.0, mean_abs_dlogp_vs_fp16=0.001)
                             for v in ("fp16", "int8_per_token", "int8_per_tensor")}
+    c["e2e_qwen_bridge"]["prompt_16384"] = {
+        v: dict(ttft_ms=900.0, graph_tpot_ms=1.01, kv_bytes=1 << 28)
+        for v in ("fp16", "int8_per_token", "int8_per_tensor")}
     c["e2e_qwen_bridge"]["setup"] = dict(model="w" * 300)
     for name in ("dense_cfg2_qwen_fp16", "dense_cfg4_llama_32k_fp16"):
         c[name] = dict(impl="sdpa", us=340.85, bytes_read=806e6, gbs=2363.0,
@@ -104,6 +108,11 @@ def test_line_is_strict_json_under_the_limit():
                  "dense_cfg2_qwen_fp16"):
         assert len(summ[name]) == 2 and summ[name][0] > 0, name
     assert "cfg5_lens" not in summ and "cfg3_int8_over_fp16_latency" not in summ
+    e2e = bench.summarize(configs)[0]   # the bridge's times per output token, both setups
+    assert e2e["e2e_qwen_bridge_int8_per_token_graph_tpot_ms"] == [0.912, None]
+    assert e2e["e2e_qwen_bridge_fp16_tpot_ms"] == [12.1, None]
+    assert e2e["e2e_qwen_bridge_prompt_16384_int8_per_tensor_graph_tpot_ms"] == [1.01, None]
+    assert not [k for k in e2e if k.startswith("e2e_qwen_bridge_setup")]
     assert back["int8_over_fp16"]["cfg3_qwen"] == 0.565
     assert "cfg4_llama_64k_splitk_p512" in back["int8_over_fp16"]
     assert math.isclose(back["int8_over_fp16"]["cfg4_llama_32k_splitk"],

@@ -362,6 +362,23 @@ def test_paged_cache_class_host_logic():
     with pytest.raises(RuntimeError, match="CUDA"):
         c.prefill(0, torch.zeros(5, 2, 128, dtype=torch.float16),
                   torch.zeros(5, 2, 128, dtype=torch.float16))
+    # the device-slot append of a captured decode step, and its host bookkeeping
+    tok = torch.zeros(2, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="prefill sets"):
+        c.append_at(1, tok, tok, torch.zeros(1, dtype=torch.int64))
+    with pytest.raises(TypeError, match="one-element int64"):
+        fp16.append_at(0, tok, tok, torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(TypeError, match="one-element int64"):
+        fp16.append_at(0, tok, tok, torch.zeros(2, dtype=torch.int64))
+    assert fp16.capacity == 2048
+    fp16.advance(2047)
+    assert fp16.lengths == [2047] * 28 and fp16.context_lens(5).tolist() == [2047]
+    with pytest.raises(AssertionError, match="full"):
+        fp16.advance(2)
+    fp16.advance(1)
+    assert fp16.lengths == [2048] * 28
+    fp16.reset()
+    assert fp16.lengths == [0] * 28
 
 
 @pytest.mark.parametrize("int8", [False, True])

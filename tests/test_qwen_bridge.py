@@ -126,6 +126,26 @@ def test_sessions_are_scoped_to_their_context():
     assert br._SESSION.get() is None
 
 
+def test_decode_graph_needs_a_prompted_session():
+    """A decode step is captured inside a session with a model, after its
+    prompt step; nothing is captured otherwise."""
+    from pa_int8 import qwen_bridge as br
+
+    class Cache:
+        is_int8 = False
+
+        def reset(self):
+            pass
+
+    with br.DecodeSession(None, Cache()) as s:
+        with pytest.raises(RuntimeError, match="after the prompt step"):
+            br.DecodeGraph(s)
+    with br.DecodeSession(object(), Cache()) as s:
+        with pytest.raises(RuntimeError, match="after the prompt step"):
+            br.DecodeGraph(s)
+        assert s._graph is None
+
+
 def test_register_is_idempotent():
     from transformers import AttentionInterface
 
