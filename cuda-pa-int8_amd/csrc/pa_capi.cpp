@@ -61,6 +61,9 @@ thread_local int g_load_mode = 0;       // 0 auto, 1 plain, 2 non-temporal cache
 thread_local int g_head_tile_cap = 0;   // 0 auto, else the most query heads per work-group
 constexpr long long kNtMinBytes = 32ll << 20;   // non-temporal loads above this much K/V
 constexpr int kKntMinPartition = 1024;          // non-temporal K rows from this split size
+// Split-K launches that read at most this much K/V (bound: every sequence at
+// the checked maximum or the block-table capacity) take the single-launch plan.
+constexpr long long kSplitKGridMaxBytes = 64ll << 20;
 // Upper bound on resident decode work-groups used to size the partial
 // buffers of the in-kernel schedule (256 CUs x 2 groups on MI355X).
 constexpr int kSchedGroupsBound = 1024;
@@ -125,6 +128,25 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // keep the grid, which saves the schedule's start-up for equal lengths.
   const int mode = g_schedule_mode;
   const long long cap = (long long)max_blocks * block_size;
+  long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
+  if (ctx < 1) ctx = 1;
+  // K/V bytes of the launch if every sequence held `ctx` tokens.
+  const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
+                             (is_f16(kind) ? 2 : 1);
+  // Split-K kinds on small launches take the single-launch plan: the host
+  // grid, splits merged in the launch, no schedule to build first.  There the
+  // schedule's start-up (context lengths, then the schedule, then the block
+  // ids) and its item floor (1536-2048 tokens per work-group) cost more than the
+  // grid's empty work-groups: every ragged launch of a few dozen MB took 18.5-20 us
+  // under the schedule.  Same box, alternating, schedule -> grid: one sequence,
+  // 12/2, 1k / 16k tokens 9.43 -> 7.48 / 12.56 -> 11.07 us (INT8 16k 14.78 ->
+  // 10.84); the reference's b1 x 4096 8/8 10.57 -> 9.04 and b8 x 4096 8/1 11.11 ->
+  // 9.80; ragged 24 x median 1024 (bound 57 MB) 19.26 -> 10.97, 4 ragged up to
+  // 9000 (37 MB) 19.18 -> 12.16; a 16k-capacity table holding 1k tokens 9.20 ->
+  // 8.12.  Past 64 MB ragged batches turn: 16 x median 2048 (164 MB) 20.5 ->
+  // 21.8, MQA 16 x median 2048 (100 MB INT8) 22.0 -> 28.9, config 5 2-4x.
+  if (mode == 0 && !is_fused(kind) && kv_bytes <= kSplitKGridMaxBytes)
+    kind = is_f16(kind) ? PA_DECODE_WARP_F16 : PA_DECODE_WARP_I8;
   p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
   // The stream partition serves the split-K kinds (its merge is the reduce
   // launch); its chunk list must count in 32 bits: at most S * ceil(cap / 32)
@@ -166,11 +188,6 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // INT8 +0.5-1.3%; FP16 with one chunk gains nothing (ragged +1.4%).
   if (ov == 0 && !is_fused(kind) && (!is_f16(kind) || p.nchunk > 1)) p.waves = 4;
   if (ov == 0 && p.stream) p.waves = 4;
-  long long ctx = max_context_len > 0 ? std::min<long long>(max_context_len, cap) : cap;
-  if (ctx < 1) ctx = 1;
-  // K/V bytes of the launch if every sequence held `ctx` tokens.
-  const long long kv_bytes = (long long)num_seqs * num_kv_heads * ctx * head_dim * 2 *
-                             (is_f16(kind) ? 2 : 1);
   // Single-launch kinds with one 16-head column tile that read enough to be
   // bandwidth-bound: one 4-wave work-group per CU, with the partition an
   // 8-wave plan would take (up to the 4-wave cap of 8192 tokens, which keeps

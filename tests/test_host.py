@@ -184,6 +184,43 @@ def test_single_launch_group_sizes(lib):
     assert p["waves"] == 8, p
 
 
+def test_small_split_k_launches_take_the_grid(lib):
+    """Split-K launches that read at most 64 MB (bound: every sequence at the
+    checked maximum, else at the table's capacity) take the single-launch
+    plan: the host grid with the splits merged in the launch, as warp /
+    warp_int8 plan the same shape; larger ones keep the in-kernel schedule.
+    Forced modes (grid = 1, schedule = 2) are left alone."""
+    info = (ctypes.c_int32 * 7)()
+
+    def plan(kind, s, h, hkv, mb, ctx):
+        assert lib.pa_decode_plan_detail(kind, s, h, 128, hkv, 16, mb, ctx, 0, info, 7) == 0
+        return tuple(info)
+
+    for splitk, warp in ((1, 0), (3, 2)):
+        for s, h, hkv, ctx in ((1, 12, 2, 1024), (1, 12, 2, 16384), (1, 8, 8, 4096),
+                               (8, 8, 1, 4096), (4, 12, 2, 9008)):
+            p = plan(splitk, s, h, hkv, (ctx + 15) // 16, ctx)
+            assert p[4] == 1 and p[6] == 1, (splitk, s, ctx, p)          # grid, merged in launch
+            assert p == plan(warp, s, h, hkv, (ctx + 15) // 16, ctx)
+        # the bound follows the checked maximum, else the table's capacity
+        assert plan(splitk, 64, 12, 2, 2048, 1024)[4] == 1               # 1024 tokens checked
+        assert plan(splitk, 64, 12, 2, 2048, 0)[4] == 2                  # 32768-token capacity
+        for s, h, hkv, ctx in ((64, 12, 2, 8192), (8, 32, 8, 32768), (256, 32, 1, 16401)):
+            assert plan(splitk, s, h, hkv, (ctx + 15) // 16, ctx)[4] == 2, (splitk, s, ctx)
+    # config 2: 128 MiB of FP16 K/V keeps the schedule; its INT8 cache is 64 MiB
+    assert plan(1, 32, 12, 2, 256, 4096)[4] == 2 and plan(3, 32, 12, 2, 256, 4096)[4] == 1
+    # exactly 64 MiB of FP16 K/V takes the grid, one block more the schedule
+    assert plan(1, 1, 8, 8, 1024, 16384)[4] == 1
+    assert plan(1, 1, 8, 8, 1025, 16400)[4] == 2
+    for mode, want in ((1, 1), (2, 2)):
+        assert lib.pa_decode_set_schedule(mode) == 0
+        try:
+            assert plan(1, 1, 12, 2, 64, 1024)[4] == want
+            assert plan(1, 1, 12, 2, 64, 1024)[6] == (1 if mode == 2 else 0)
+        finally:
+            lib.pa_decode_set_schedule(0)
+
+
 def test_waves_override_hook(lib):
     assert lib.pa_decode_set_waves_per_group(3) == 2
     for w in (4, 8, 0):
