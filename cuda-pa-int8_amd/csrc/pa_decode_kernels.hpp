@@ -1523,6 +1523,7 @@ struct SchedArgs {
   int rows_max;       // slot rows the partial buffers hold
   int pmin, pmax;     // partition bounds (multiples of kIterTokens)
   int pmin_uniform;   // lower bound when all lengths are equal (one item per work-group)
+  float fill_scale;   // 1024 * kv heads * head chunks / CUs (see the ragged floor below)
 };
 
 constexpr int kShortBuckets = 4;   // (their counts pack into one 64-bit word)
@@ -1672,7 +1673,13 @@ __device__ __forceinline__ Schedule build_schedule_small(const int* __restrict__
                                        (float)(groups * k));
     uint64_t part = (uint64_t)fminf(want, (float)sa.pmax);
     part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
-    const uint64_t lo = sc.uniform ? (uint64_t)sa.pmin_uniform : (uint64_t)sa.pmin;
+    uint64_t lo = (uint64_t)sa.pmin_uniform;   // (the same bounds as build_schedule's)
+    if (!sc.uniform) {
+      uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
+                                   (float)sa.pmin);
+      f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
+      lo = f < lo ? lo : f;
+    }
     part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
     const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
     sc.partition = (int)(part < top ? part : top);
@@ -1791,8 +1798,20 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
     part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
     // The ragged lower bound keeps items of a few hundred tokens from paying
     // their fixed costs too often; with equal lengths every resident
-    // work-group gets one item, so the smaller grid bound applies.
-    const uint64_t lo = sc.uniform ? (uint64_t)sa.pmin_uniform : (uint64_t)sa.pmin;
+    // work-group gets one item, so the smaller grid bound applies.  A ragged
+    // launch with less work than one pmin item per CU lowers the bound to about
+    // one item per CU (its token total is below (t + S) * 1024), down to the
+    // equal-length bound: same box, alternating, 16 ragged sequences of median
+    // 2048 at 12/2 20.48 -> 17.00 us (INT8 19.53 -> 14.53), 48 of median 512
+    // 19.52 -> 12.87, MQA 32/1 16 x median 2048 INT8 22.08 -> 17.54.  Config 5
+    // keeps its partitions (0.2-1.1% slower with the extra code).
+    uint64_t lo = (uint64_t)sa.pmin_uniform;
+    if (!sc.uniform) {
+      uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
+                                   (float)sa.pmin);
+      f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
+      lo = f < lo ? lo : f;
+    }
     part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
     const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
     sc.partition = (int)(part < top ? part : top);
@@ -2343,7 +2362,11 @@ hipError_t launch_decode_tiles(const DecodeLaunch& l) {
     return hipGetLastError();
   }
   if (l.sched) {
-    const SchedArgs sa{l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform};
+    constexpr int kGroupsPerCU = kWavesPerCU / NW;
+    const int cus = (l.groups + kGroupsPerCU - 1) / kGroupsPerCU;
+    const SchedArgs sa{l.queue, l.rows_max, l.pmin, l.pmax, l.pmin_uniform,
+                       1024.f * (float)(l.shape.num_kv_heads * l.shape.nchunk) /
+                           (float)(cus > 0 ? cus : 1)};
     const auto* q = static_cast<const half_t*>(l.q);
     const auto* kc = static_cast<const uint8_t*>(l.k_cache);
     const auto* vc = static_cast<const uint8_t*>(l.v_cache);
