@@ -1673,13 +1673,11 @@ __device__ __forceinline__ Schedule build_schedule_small(const int* __restrict__
                                        (float)(groups * k));
     uint64_t part = (uint64_t)fminf(want, (float)sa.pmax);
     part = (part + kIterTokens - 1) / kIterTokens * kIterTokens;
-    uint64_t lo = (uint64_t)sa.pmin_uniform;   // (the same bounds as build_schedule's)
-    if (!sc.uniform) {
-      uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
-                                   (float)sa.pmin);
-      f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
-      lo = f < lo ? lo : f;
-    }
+    // (the same bounds as build_schedule's)
+    uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
+                                 (float)sa.pmin);
+    f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
+    const uint64_t lo = (sc.uniform || f < (uint64_t)sa.pmin_uniform) ? (uint64_t)sa.pmin_uniform : f;
     part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
     const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
     sc.partition = (int)(part < top ? part : top);
@@ -1804,14 +1802,13 @@ __device__ Schedule build_schedule(const int* __restrict__ ctxl, const DecodeSha
     // equal-length bound: same box, alternating, 16 ragged sequences of median
     // 2048 at 12/2 20.48 -> 17.00 us (INT8 19.53 -> 14.53), 48 of median 512
     // 19.52 -> 12.87, MQA 32/1 16 x median 2048 INT8 22.08 -> 17.54.  Config 5
-    // keeps its partitions (0.2-1.1% slower with the extra code).
-    uint64_t lo = (uint64_t)sa.pmin_uniform;
-    if (!sc.uniform) {
-      uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
-                                   (float)sa.pmin);
-      f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
-      lo = f < lo ? lo : f;
-    }
+    // keeps its partitions and its times (within 0.5%).
+    // (branch-free: both bounds are cheap scalar values; a branch here cost the
+    // scheduled launches 0.2-1.1% through code layout alone)
+    uint64_t f = (uint64_t)fminf(__builtin_ceilf((float)(t + (uint32_t)S) * sa.fill_scale),
+                                 (float)sa.pmin);
+    f = (f + kIterTokens - 1) / kIterTokens * kIterTokens;
+    const uint64_t lo = (sc.uniform || f < (uint64_t)sa.pmin_uniform) ? (uint64_t)sa.pmin_uniform : f;
     part = part < lo ? lo : (part > (uint64_t)sa.pmax ? (uint64_t)sa.pmax : part);
     const uint64_t top = ((uint64_t)(b > 0 ? b : 1) + kIterTokens - 1) / kIterTokens * kIterTokens;
     sc.partition = (int)(part < top ? part : top);
