@@ -263,3 +263,66 @@ def test_schedule_forced_partition(partition):
     for variant in ("warp", "splitk"):
         assert_close(run(c, variant, partition=partition), oracle_fp16(c),
                      what=f"P={partition} {variant}")
+
+
+def _distribution(c, variant, mb, ctx=0):
+    """The planner's work distribution (1 grid, 2 schedule) for case `c`."""
+    import ctypes
+
+    import pa_int8
+
+    kind = {"warp": 0, "splitk": 1, "warp_int8": 2, "splitk_int8": 3}[variant]
+    info = (ctypes.c_int32 * 7)()
+    S, H, D = c["q"].shape
+    Hkv = c["k_cache"].shape[1]
+    assert pa_int8.capi().pa_decode_plan_detail(kind, S, H, D, Hkv, c["block_size"], mb, ctx,
+                                                0, info, 7) == 0
+    return info[4]
+
+
+@pytest.mark.parametrize("variant", ["splitk", "splitk_int8"])
+@pytest.mark.parametrize("extra_blocks", [0, 1])
+def test_split_k_small_launch_boundary(variant, extra_blocks):
+    """Split-K calls reading at most 64 MiB of K/V (bound: the table's
+    capacity for the no-check entry) take the single-launch plan; one block
+    more of capacity and they keep the in-kernel schedule.  Both sides give
+    the oracle's result, with short ragged sequences in a capacity-sized table."""
+    _mode(0)
+    int8 = variant.endswith("int8")
+    lens = ragged_lens(4, seed=31, hi=2500)
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, 8, 8, seed=31)
+    # FP16 K/V of 4 sequences x 8 kv heads x 4096 tokens x 128 dims is 64 MiB; INT8 at 8192
+    cap_blocks = (512 if int8 else 256) + extra_blocks
+    table = c["block_table8"] if int8 else c["block_table"]
+    bt = np.zeros((len(lens), cap_blocks), np.int32)
+    bt[:, :table.shape[1]] = table
+    assert _distribution(c, variant, cap_blocks) == (2 if extra_blocks else 1)
+    want = (oracle_int8 if int8 else oracle_fp16)(c)
+    assert_close(run(c, variant, bt=bt, check=False, int8=int8), want,
+                 what=f"{variant} capacity {cap_blocks} blocks")
+
+
+@pytest.mark.parametrize("variant", ["splitk", "splitk_int8"])
+@pytest.mark.parametrize("heads", [(12, 2), (32, 1)])
+def test_ragged_floor_below_one_item_per_cu(variant, heads):
+    """A ragged launch with less work than one floor-sized item per CU (16
+    sequences of median 2048 tokens) runs items of about one per CU; the
+    result is the oracle's, and bitwise equal to the forced-schedule run
+    at the same partition choice."""
+    _mode(0)
+    int8 = variant.endswith("int8")
+    rng = np.random.default_rng(41)
+    lens = np.clip(np.round(np.exp(rng.normal(math.log(2048), 1.0, 16))), 16, 12000).astype(np.int32)
+    h, hkv = heads
+    c = (int8_case if int8 else fp16_case)(len(lens), lens, h, hkv, seed=41)
+    table = c["block_table8"] if int8 else c["block_table"]
+    # a table sized for 32k tokens: past the 64 MiB bound of the single-launch plan
+    bt = np.zeros((len(lens), 2048), np.int32)
+    bt[:, :table.shape[1]] = table
+    assert _distribution(c, variant, bt.shape[1]) == 2
+    want = (oracle_int8 if int8 else oracle_fp16)(c)
+    got = run(c, variant, bt=bt, check=False, int8=int8)
+    assert_close(got, want, what=f"{variant} {h}/{hkv}")
+    _mode(SCHED)
+    again = run(c, variant, bt=bt, check=False, int8=int8)
+    assert np.array_equal(got, again)
