@@ -326,3 +326,37 @@ def test_ragged_floor_below_one_item_per_cu(variant, heads):
     _mode(SCHED)
     again = run(c, variant, bt=bt, check=False, int8=int8)
     assert np.array_equal(got, again)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_checked_equal_lengths_take_the_single_launch_plan(int8):
+    """The reference-named split-K ops read the lengths for their `min >= 1`
+    check; with equal lengths they run the single-launch plan, so their output
+    is bitwise the single-launch op's, and the oracle's within tolerance.
+    Ragged lengths keep the split-K plan."""
+    from pa_int8 import registry
+
+    _mode(0)
+    for lens, equal in ((np.full(6, 3000, np.int32), True),
+                        (np.array([3000, 2999, 3000, 100, 3000, 3000], np.int32), False)):
+        c = (int8_case if int8 else fp16_case)(len(lens), lens, 12, 2, seed=43)
+        want = (oracle_int8 if int8 else oracle_fp16)(c)
+        q = _t(c["q"])
+        outs = {}
+        for name in (("warp_int8", "splitk_int8") if int8 else ("warp", "splitk")):
+            out = torch.empty_like(q)
+            if int8:
+                registry.VARIANTS_INT8[name](out, q, _t(c["k_cache8"]), _t(c["v_cache8"]),
+                                             _t(c["k_scales"]), _t(c["v_scales"]),
+                                             _t(c["block_table8"]), _t(lens), c["scale"],
+                                             c["block_size"])
+            else:
+                registry.VARIANTS[name](out, q, _t(c["k_cache"]), _t(c["v_cache"]),
+                                        _t(c["block_table"]), _t(lens), c["scale"],
+                                        c["block_size"])
+            torch.cuda.synchronize()
+            outs[name] = out.float().cpu().numpy()
+            assert_close(outs[name], want, what=f"{name} equal={equal}")
+        a, b = outs.values()
+        if equal:
+            assert np.array_equal(a, b)
