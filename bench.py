@@ -554,6 +554,53 @@ def run_dense_baseline(torch, name, lens, h, hkv, d, steps, warmup, outliers=Fal
     return res
 
 
+def _bridge_model(torch, seed):
+    """The random-init Qwen2.5-1.5B-shape model (fp16, 28 layers, 12 q / 2 kv
+    heads, head_dim 128, vocab 151936) on the bridge's attention interface."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from pa_int8 import qwen_bridge as br
+
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
+                      max_position_embeddings=32768, rope_theta=1e6, tie_word_embeddings=True)
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg).to(torch.float16).eval()
+    br.register()
+    model.set_attn_implementation(br.ATTN_NAME)
+    return model, cfg
+
+
+def _bridge_cache(variant, n):
+    from pa_int8 import PagedKVCache
+
+    return PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128, max_len=n, variant=variant)
+
+
+def run_e2e_long(torch, long_len=16384, max_new=64, seed=0):
+    """Only the graph-replayed decode after a `long_len`-token prompt, FP16 and
+    INT8 (per-token) caches, two passes: the workload of the bridge's kernel
+    trace at a long context (`--configs e2elong` under rocprofv3)."""
+    from pa_int8 import qwen_bridge as br
+
+    model, cfg = _bridge_model(torch, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    prompt = torch.randint(0, cfg.vocab_size, (1, long_len), generator=g).cuda()
+    res = {}
+    for rep in range(2):
+        for variant in ("fp16", "int8_per_token"):
+            cache = _bridge_cache(variant, long_len + max_new)
+            _, ttft, tpot, _ = br.generate_greedy_graph(model, prompt, max_new, cache)
+            res[f"{variant}_pass{rep}"] = dict(ttft_ms=round(ttft * 1e3, 2),
+                                               graph_tpot_ms=round(tpot * 1e3, 3))
+            log(f"[bench] e2e long {long_len} {variant} pass {rep}: TPOT {tpot * 1e3:.3f} ms graph")
+            del cache
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0, long_len=16384):
     """End-to-end greedy decode of a random-init Qwen2.5-1.5B-shape model (fp16,
     28 layers, 12 q / 2 kv heads, head_dim 128, vocab 151936) through the
@@ -567,26 +614,13 @@ def run_e2e_bridge(torch, prompt_len=1024, max_new=64, seed=0, long_len=16384):
     `long_len`-token prompt, graph replays only, where the cache's bytes are a
     visible share of each token's reads.  No checkpoint is available offline,
     so perplexity itself is not meaningful here and is not reported."""
-    from transformers import Qwen2Config, Qwen2ForCausalLM
-
-    from pa_int8 import PagedKVCache
     from pa_int8 import qwen_bridge as br
 
-    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
-                      num_hidden_layers=28, num_attention_heads=12, num_key_value_heads=2,
-                      max_position_embeddings=32768, rope_theta=1e6, tie_word_embeddings=True)
-    torch.manual_seed(seed)
-    with torch.device("cuda"):
-        model = Qwen2ForCausalLM(cfg).to(torch.float16).eval()
-    br.register()
-    model.set_attn_implementation(br.ATTN_NAME)
+    model, cfg = _bridge_model(torch, seed)
     g = torch.Generator().manual_seed(seed)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g).cuda()
     variants = ("fp16", "int8_per_token", "int8_per_tensor")
-
-    def new_cache(variant, n):
-        return PagedKVCache(num_layers=28, num_kv_heads=2, head_dim=128, max_len=n,
-                            variant=variant)
+    new_cache = _bridge_cache
 
     res = {}
     ref_tokens = ref_lp = None
@@ -813,6 +847,8 @@ def run_configs(torch, names, steps, warmup):
                             "reference's GB/s does (bench_paged_decode.py:148-152)")
     if "e2e" in names:
         out["e2e_qwen_bridge"] = run_e2e_bridge(torch)
+    if "e2elong" in names:
+        out["e2e_long_context"] = run_e2e_long(torch)
     if "dense" in names:
         out["dense_cfg2_qwen_fp16"] = run_dense_baseline(torch, "cfg2", [4096] * 32, 12, 2, 128,
                                                          steps_for(150, steps), warmup)
@@ -1124,7 +1160,9 @@ def main():
     ap.add_argument("--configs", default="all",
                     help="comma list of " + ",".join(ALL_CONFIGS) + " or 'all'; also "
                     "cfg5counters (config 5's decode launches for rocprofv3 counters, untimed), "
-                    "counters (those and the other kernels the counter summaries cover)")
+                    "counters (those and the other kernels the counter summaries cover), "
+                    "e2elong (the bridge's graph-replayed decode after a 16k prompt only, "
+                    "for a kernel trace)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
