@@ -143,8 +143,9 @@ Plan make_plan(pa_decode_kind_t kind, int num_seqs, int num_heads, int num_kv_he
   // 10.84); the reference's b1 x 4096 8/8 10.57 -> 9.04 and b8 x 4096 8/1 11.11 ->
   // 9.80; ragged 24 x median 1024 (bound 57 MB) 19.26 -> 10.97, 4 ragged up to
   // 9000 (37 MB) 19.18 -> 12.16; a 16k-capacity table holding 1k tokens 9.20 ->
-  // 8.12.  Past 64 MB ragged batches turn: 16 x median 2048 (164 MB) 20.5 ->
-  // 21.8, MQA 16 x median 2048 (100 MB INT8) 22.0 -> 28.9, config 5 2-4x.
+  // 8.12.  Past 64 MB ragged batches turn (against the schedule with its
+  // load-aware floor): 16 x median 2048 (164 MB) 17.0 -> 21.8, MQA 16 x median
+  // 2048 (100 MB INT8) 17.5 -> 28.9, config 5 2-4x.
   if (mode == 0 && !is_fused(kind) && kv_bytes <= kSplitKGridMaxBytes)
     kind = is_f16(kind) ? PA_DECODE_WARP_F16 : PA_DECODE_WARP_I8;
   p.sched = mode == 2 || (mode == 0 && !is_fused(kind));
