@@ -3,9 +3,10 @@
 // Work decomposition
 //   A work item is (sequence, kv_head, split).  A work-group of 4 or 8 waves serves
 //   one work item for the whole group of query heads that share the kv head
-//   (up to 16), so every K/V byte fetched from HBM feeds all of them (the
-//   reference launches one block per query head and re-reads KV G times,
-//   kernels/paged_attention_v3_warp.cu:159).  The split's tokens are cut into
+//   (up to 16 per MFMA column tile, two tiles at head_dim <= 128; larger
+//   groups in several head chunks), so every K/V byte fetched from HBM feeds
+//   all of them (the reference launches one block per query head and re-reads
+//   KV G times, kernels/paged_attention_v3_warp.cu:159).  The split's tokens are cut into
 //   wave iterations (64 tokens for head_dim <= 128, else 32) dealt
 //   round-robin to the waves (a fixed assignment, so results are bitwise
 //   reproducible); each wave keeps its own online-softmax state and the waves
@@ -41,11 +42,12 @@
 //   stay normal and below fp16's range; the running sum l accumulates the
 //   unscaled weight.
 //
-// Splits: FUSED (the single-launch warp variant) writes per-split partials
-//   with device-coherent (write-through) stores, waits for them, counts
-//   arrivals with a device-scope atomic, and the last work-group of a unit
-//   merges with device-coherent loads in the same launch.  Otherwise
-//   (split-K) a separate reduce kernel merges the partials
+// Splits: FUSED (the single-launch grid kernel, and the scheduled split-K
+//   kernel) writes per-split partials with device-coherent (write-through)
+//   stores, waits for them, counts arrivals with a device-scope atomic, and
+//   the last work-group of a unit merges with device-coherent loads in the
+//   same launch (units with many splits in two levels).  The grid and stream
+//   forms of split-K merge in a separate reduce kernel
 //   (paged_attention_v4_splitk.cu:156-187).
 #pragma once
 
